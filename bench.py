@@ -1,0 +1,350 @@
+"""Benchmark of the MI355X hip backend on BASELINE.json's metric.
+
+Headline (``value``): fp32 GEMM 8192^3 GFLOP/s through ``a @ b`` (config 4),
+inputs resident in HBM, one step = one product. ``extra`` holds the other
+hot-path workloads of the metric ("+ GEMV/norm HBM GB/s") and the remaining
+configs (GEMV/DOT, scaled norms, RNG, fp64/padded/batched GEMM, compiled MLP),
+each with its roofline fraction. Kernel durations come from HIP events
+recorded on the library's stream around the timed region.
+
+Usage: python bench.py [--gpus 1] [--steps K] [--warmup W] [--skip-cpu] [--only NAME,...]
+Prints ONE JSON line on stdout; progress goes to stderr.
+"""
+
+import argparse
+import ctypes
+import json
+import os
+import sys
+import time
+from pathlib import Path
+
+ROOT = Path(__file__).resolve().parent
+for _path in (str(ROOT / "open-pacho_amd"), str(ROOT)):
+    if _path not in sys.path:
+        sys.path.insert(0, _path)
+
+import numpy as np  # noqa: E402
+
+METRIC = "fp32 GEMM GFLOP/s @8192³ + GEMV/norm HBM GB/s, % of MI355X roofline"
+PEAK_HBM_GBS = 8000.0
+PEAK_FP32_TFLOPS = 157.3
+PEAK_FP64_TFLOPS = 78.6
+
+
+def log(message):
+    print(f"[bench] {message}", file=sys.stderr, flush=True)
+
+
+class Timer:
+    """HIP events on the backend stream around a region of repeated calls."""
+
+    def __init__(self, backend):
+        self.backend = backend
+        lib, ctx = backend._lib, backend._ctx
+        self.start, self.stop = ctypes.c_void_p(), ctypes.c_void_p()
+        assert lib.hp_event_create(ctx, ctypes.byref(self.start)) == 0
+        assert lib.hp_event_create(ctx, ctypes.byref(self.stop)) == 0
+
+    def run(self, fn, reps, warmup=2):
+        lib, ctx = self.backend._lib, self.backend._ctx
+        for _ in range(warmup):
+            fn()
+        self.backend.synchronize()
+        wall0 = time.perf_counter()
+        lib.hp_event_record(ctx, self.start)
+        for _ in range(reps):
+            fn()
+        lib.hp_event_record(ctx, self.stop)
+        self.backend.synchronize()
+        wall = (time.perf_counter() - wall0) * 1e3 / reps
+        ms = ctypes.c_float()
+        assert lib.hp_event_elapsed_ms(self.start, self.stop, ctypes.byref(ms)) == 0
+        return ms.value / reps, wall
+
+
+def roofline(bound, work, ms, traffic=None):
+    if bound == "hbm":
+        achieved = work / (ms * 1e-3) / 1e9
+        peak, unit = PEAK_HBM_GBS, "GB/s"
+    else:
+        achieved = work / (ms * 1e-3) / 1e12
+        peak, unit = (PEAK_FP64_TFLOPS if bound == "mfma_fp64" else PEAK_FP32_TFLOPS), "TFLOP/s"
+        bound = "mfma"
+    return {"bound": bound, "achieved": round(achieved, 3), "peak": peak, "unit": unit, "frac": round(achieved / peak, 4), "traffic": traffic}
+
+
+def _traffic(name):
+    """HBM bytes per launch measured by rocprofv3 --pmc (profiles/traffic.json), if recorded."""
+    path = ROOT / "profiles" / "traffic.json"
+    if not path.exists():
+        return None
+    try:
+        return json.loads(path.read_text()).get(name, {}).get("bytes_per_launch")
+    except (OSError, ValueError):
+        return None
+
+
+def cpu_threads():
+    try:
+        return len(os.sched_getaffinity(0))
+    except AttributeError:
+        return os.cpu_count() or 1
+
+
+def bench_gemm(p, hip, steps, warmup):
+    n = 8192
+    rng = p.random.default_rng(3, backend=hip)
+    a = rng.uniform(-1, 1, (n, n), dtype="float32")
+    b = rng.uniform(-1, 1, (n, n), dtype="float32")
+    timer = Timer(hip)
+    for _ in range(warmup):
+        a @ b
+    hip.synchronize()
+    wall0 = time.perf_counter()
+    lib, ctx = hip._lib, hip._ctx
+    lib.hp_event_record(ctx, timer.start)
+    for _ in range(steps):
+        c = a @ b
+    lib.hp_event_record(ctx, timer.stop)
+    hip.synchronize()
+    wall_ms = (time.perf_counter() - wall0) * 1e3 / steps
+    ms = ctypes.c_float()
+    lib.hp_event_elapsed_ms(timer.start, timer.stop, ctypes.byref(ms))
+    kernel_ms = ms.value / steps
+    flops = 2.0 * n**3
+    del c
+    return {"a": a, "b": b, "flops": flops, "kernel_ms": kernel_ms, "wall_ms": wall_ms}
+
+
+def cpu_gemm_baseline(p, gemm):
+    """np.matmul (the reference NumPy backend's path) on a row sample of the same product."""
+    from oracle import numpy_backend
+
+    rows = int(os.environ.get("PACHO_BENCH_CPU_ROWS", "1024"))
+    a = p.asnumpy(gemm["a"][:rows])
+    b = p.asnumpy(gemm["b"])
+    numpy_backend.matmul(a[:64], b)  # warm the BLAS thread pool
+    reps, t0 = 0, time.perf_counter()
+    while reps < 3 or time.perf_counter() - t0 < 8.0:
+        numpy_backend.matmul(a, b)
+        reps += 1
+    seconds = (time.perf_counter() - t0) / reps
+    gflops = 2.0 * rows * 8192 * 8192 / seconds / 1e9
+    try:
+        from threadpoolctl import threadpool_info
+
+        threads = max((i.get("num_threads", 1) for i in threadpool_info() if i.get("user_api") == "blas"), default=1)
+    except Exception:  # noqa: BLE001
+        threads = cpu_threads()
+    return {
+        "value": round(gflops, 2),
+        "unit": "GFLOP/s",
+        "cores": int(threads),
+        "kind": "port",
+        "sample": f"np.matmul float32 A[:{rows}] @ B (8192x8192), {reps} reps (mean)",
+    }
+
+
+def bench_extras(p, hip, only, skip_cpu):
+    from oracle import numpy_backend
+
+    timer = Timer(hip)
+    extra = {}
+
+    def want(name):
+        return not only or name in only
+
+    if want("gemv"):
+        n = 16384
+        rng = p.random.default_rng(1, backend=hip)
+        A = rng.uniform(-1, 1, (n, n), dtype="float32")
+        x = rng.normal(0, 1, n, dtype="float32")
+        ms, wall = timer.run(lambda: A @ x, 20)
+        bytes_moved = n * n * 4 + 2 * n * 4
+        extra["gemv_f32_16384"] = {
+            "value": round(bytes_moved / (ms * 1e-3) / 1e9, 1),
+            "unit": "GB/s",
+            "kernel_us": round(ms * 1e3, 2),
+            "wall_us": round(wall * 1e3, 2),
+            "roofline": roofline("hbm", bytes_moved, ms, _traffic("gemv")),
+        }
+        ms, wall = timer.run(lambda: p.dot(x, x), 50)
+        extra["dot_f32_16384"] = {"value": round(ms * 1e3, 2), "unit": "us", "wall_us": round(wall * 1e3, 2)}
+        if not skip_cpu:
+            host_a, host_x = p.asnumpy(A), p.asnumpy(x)
+            reps, t0 = 0, time.perf_counter()
+            while reps < 3 or time.perf_counter() - t0 < 3.0:
+                numpy_backend.matmul(host_a, host_x)
+                reps += 1
+            sec = (time.perf_counter() - t0) / reps
+            extra["gemv_f32_16384"]["cpu_baseline"] = {"value": round(bytes_moved / sec / 1e9, 2), "unit": "GB/s", "cores": cpu_threads(), "kind": "port"}
+            del host_a
+        del A
+    if want("norm"):
+        n = 1 << 28
+        for dtype, decades in (("float32", 30.0), ("float64", 300.0)):
+            rng = p.random.default_rng(2, backend=hip)
+            mags = p.power(10.0 if dtype == "float64" else np.float32(10.0), rng.uniform(-decades, decades, n, dtype=dtype))
+            signs = rng.random(n, dtype=dtype) < 0.5
+            x = p.where(signs, -mags, mags)
+            del mags, signs
+            ms, wall = timer.run(lambda: p.linalg.norm(x), 10)
+            bytes_moved = n * np.dtype(dtype).itemsize
+            key = f"norm_flat_{dtype}_2^28"
+            extra[key] = {
+                "value": round(bytes_moved / (ms * 1e-3) / 1e9, 1),
+                "unit": "GB/s",
+                "kernel_us": round(ms * 1e3, 2),
+                "wall_us": round(wall * 1e3, 2),
+                "roofline": roofline("hbm", bytes_moved, ms, _traffic(f"norm_{dtype}")),
+            }
+            if not skip_cpu:
+                sample = p.asnumpy(x[: 1 << 24])
+                t0 = time.perf_counter()
+                numpy_backend.norm(sample)
+                sec = time.perf_counter() - t0
+                extra[key]["cpu_baseline"] = {"value": round(sample.nbytes / sec / 1e9, 2), "unit": "GB/s", "cores": 1, "kind": "port", "sample": "two-pass NumPy norm of 2^24 elements"}
+            del x
+        rows = p.random.default_rng(2, backend=hip).uniform(-1, 1, (65536, 4096), dtype="float32")
+        ms, wall = timer.run(lambda: p.linalg.norm(rows, axis=1), 10)
+        bytes_moved = 65536 * 4096 * 4 + 65536 * 4
+        extra["norm_rows_f32_65536x4096"] = {
+            "value": round(bytes_moved / (ms * 1e-3) / 1e9, 1),
+            "unit": "GB/s",
+            "kernel_us": round(ms * 1e3, 2),
+            "roofline": roofline("hbm", bytes_moved, ms, _traffic("norm_rows")),
+        }
+        del rows
+    if want("rng"):
+        n = 1 << 28
+        for dist in ("uniform", "normal", "exponential"):
+            rng = p.random.default_rng(42, backend=hip)
+            ms, wall = timer.run(lambda: getattr(rng, dist)(size=n, dtype="float32"), 10)
+            bytes_moved = n * 4
+            extra[f"rng_{dist}_f32_2^28"] = {
+                "value": round(n / (ms * 1e-3) / 1e9, 2),
+                "unit": "Gsample/s",
+                "kernel_us": round(ms * 1e3, 2),
+                "roofline": roofline("hbm", bytes_moved, ms, _traffic(f"rng_{dist}")),
+                "alu_bound_note": "20 32x32->64 integer multiplies per Philox4x32-10 block, one block per sample",
+            }
+        if not skip_cpu:
+            count = 1 << 22
+            t0 = time.perf_counter()
+            numpy_backend.random("normal", "float32", (count,), 42)
+            sec = time.perf_counter() - t0
+            extra["rng_normal_f32_2^28"]["cpu_baseline"] = {"value": round(count / sec / 1e9, 4), "unit": "Gsample/s", "cores": 1, "kind": "port", "sample": "NumPy Philox normal, 2^22 samples"}
+    if want("gemm_f64"):
+        n = 4096
+        rng = p.random.default_rng(3, backend=hip)
+        a = rng.uniform(-1, 1, (n, n), dtype="float64")
+        b = rng.uniform(-1, 1, (n, n), dtype="float64")
+        ms, wall = timer.run(lambda: a @ b, 5)
+        flops = 2.0 * n**3
+        extra["gemm_f64_4096"] = {"value": round(flops / (ms * 1e-3) / 1e9, 1), "unit": "GFLOP/s", "kernel_ms": round(ms, 4), "roofline": roofline("mfma_fp64", flops, ms)}
+        del a, b
+    if want("gemm_padded"):
+        m, k, n = 4097, 3001, 2049
+        rng = p.random.default_rng(3, backend=hip)
+        a = rng.uniform(-1, 1, (m, k), dtype="float32")
+        b = rng.uniform(-1, 1, (k, n), dtype="float32")
+        ms, wall = timer.run(lambda: p.matmul(a, b, padding=True), 10)
+        flops = 2.0 * m * n * k
+        extra["gemm_f32_4097x3001x2049_padded"] = {"value": round(flops / (ms * 1e-3) / 1e9, 1), "unit": "GFLOP/s", "kernel_ms": round(ms, 4), "roofline": roofline("mfma", flops, ms)}
+        ms, wall = timer.run(lambda: a @ b, 10)
+        extra["gemm_f32_4097x3001x2049_unpadded"] = {"value": round(flops / (ms * 1e-3) / 1e9, 1), "unit": "GFLOP/s", "kernel_ms": round(ms, 4), "roofline": roofline("mfma", flops, ms)}
+        del a, b
+    if want("gemm_batched"):
+        rng = p.random.default_rng(3, backend=hip)
+        a = rng.uniform(-1, 1, (64, 512, 1024), dtype="float32")
+        b = rng.uniform(-1, 1, (1024, 768), dtype="float32")
+        ms, wall = timer.run(lambda: a @ b, 10)
+        flops = 2.0 * 64 * 512 * 768 * 1024
+        extra["gemm_f32_batched_64x512x1024x768"] = {"value": round(flops / (ms * 1e-3) / 1e9, 1), "unit": "GFLOP/s", "kernel_ms": round(ms, 4), "roofline": roofline("mfma", flops, ms)}
+        del a, b
+    if want("mlp"):
+        rng = p.random.default_rng(42, backend=hip)
+        widths = (4096, 4096, 4096, 1024)
+        params = []
+        for fan_in, fan_out in zip(widths[:-1], widths[1:]):
+            params.append(rng.normal(0, (1 / fan_in) ** 0.5, (fan_in, fan_out), dtype="float32"))
+            params.append(p.zeros(fan_out, dtype=np.float32, backend=hip))
+        x = rng.uniform(-1, 1, (8192, 4096), dtype="float32")
+
+        @p.compile
+        def mlp(x, w1, b1, w2, b2, w3, b3):
+            h = p.tanh(x @ w1 + b1)
+            h = p.tanh(h @ w2 + b2)
+            out = p.tanh(h @ w3 + b3)
+            return p.mean(out, axis=1)
+
+        ms, wall = timer.run(lambda: mlp(x, *params), 5)
+        flops = 2.0 * 8192 * (4096 * 4096 * 2 + 4096 * 1024)
+        extra["mlp_forward_f32_8192x4096"] = {
+            "value": round(flops / (ms * 1e-3) / 1e9, 1),
+            "unit": "GFLOP/s",
+            "kernel_ms": round(ms, 4),
+            "wall_ms": round(wall, 4),
+            "steps": [s["kind"] for s in mlp.explain(x, *params)["steps"]],
+            "roofline": roofline("mfma", flops, ms),
+        }
+    return extra
+
+
+def main(argv=None):
+    parser = argparse.ArgumentParser(description=__doc__.splitlines()[0])
+    parser.add_argument("--gpus", type=int, default=1)
+    parser.add_argument("--steps", type=int, default=10)
+    parser.add_argument("--warmup", type=int, default=3)
+    parser.add_argument("--skip-cpu", action="store_true", help="omit the CPU baselines")
+    parser.add_argument("--only", default="", help="comma-separated extras to run (gemv,norm,rng,gemm_f64,gemm_padded,gemm_batched,mlp); 'none' for the headline only")
+    args = parser.parse_args(argv)
+    if args.gpus != 1:
+        print(
+            f"bench.py measures one MI355X: this build has no multi-GPU path (asked for --gpus {args.gpus}). "
+            "Run with --gpus 1.",
+            file=sys.stderr,
+        )
+        return 2
+    import openpacho as p
+
+    hip = p.get_backend("hip", device=0)
+    log(f"device {hip.device}; GEMM 8192^3 fp32, warmup {args.warmup}, steps {args.steps}")
+    gemm = bench_gemm(p, hip, args.steps, args.warmup)
+    gflops = gemm["flops"] / (gemm["wall_ms"] * 1e-3) / 1e9
+    log(f"gemm: kernel {gemm['kernel_ms']:.3f} ms, wall {gemm['wall_ms']:.3f} ms, {gflops:.0f} GFLOP/s")
+    cpu = None
+    if not args.skip_cpu:
+        log("cpu baseline: np.matmul row sample")
+        cpu = cpu_gemm_baseline(p, gemm)
+    del gemm["a"], gemm["b"]
+    only = set() if not args.only else {s.strip() for s in args.only.split(",") if s.strip()}
+    extra = {} if only == {"none"} else bench_extras(p, hip, only, args.skip_cpu)
+    for name, entry in extra.items():
+        log(f"{name}: {entry['value']} {entry['unit']}" + (f" ({entry['roofline']['frac']:.1%} of roofline)" if "roofline" in entry else ""))
+    result = {
+        "metric": METRIC,
+        "value": round(gflops, 1),
+        "unit": "GFLOP/s",
+        "n_gpus": 1,
+        "steps": args.steps,
+        "warmup": args.warmup,
+        "ms_per_step": round(gemm["wall_ms"], 4),
+        "higher_is_better": True,
+        "scaling": "weak",
+        "vs_baseline": None,
+        "dtype": "f32",
+        "data": "synthetic: on-device Philox4x32-10 U[-1,1) float32, seed 3 (inputs resident in HBM)",
+        "config": {"workload": "fp32 GEMM C = A @ B, 8192x8192x8192, row-major (BASELINE config 4)", "parallelism": "single GPU"},
+        "roofline": roofline("mfma", gemm["flops"], gemm["kernel_ms"], _traffic("gemm_f32")),
+        "cpu_baseline": cpu,
+        "kernel_ms_per_step": round(gemm["kernel_ms"], 4),
+        "extra": extra,
+    }
+    print(json.dumps(result), flush=True)
+    return 0
+
+
+if __name__ == "__main__":
+    sys.exit(main())

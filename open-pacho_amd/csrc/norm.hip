@@ -1,0 +1,281 @@
+// Overflow/underflow-safe Euclidean norms (fp32/fp64) with one HBM read.
+//
+// Contiguous rows (inner == 1): one wave owns a chunk of kChunk<T> elements,
+// loads it into registers with 16-byte nontemporal loads, then runs the two
+// classic passes on the registers: (1) m = max|x| with NaN propagation, (2)
+// t = sum (x * 2^-e)^2 where m = f * 2^e, f in [0.5, 1). Scaling by a power of
+// two is exact, so the only roundings are the squares and the sum; t <= len.
+// A chunk's result is the pair (e, t), i.e. norm^2 = 4^e * t. Pairs merge
+// exactly by rescaling with powers of two, and the final value is
+// ldexp(sqrt(t), e). Special pairs: NaN chunk -> (NaN, 0); Inf (no NaN) ->
+// (+inf, 0); all-zero -> (-inf, 0).
+//
+// Reference semantics: _norm.py:28-36 (NaN beats Inf, Inf -> Inf, zeros -> +0),
+// _norm.py:44-52 (two-pass max-scale closed form), linalg.py:8-35.
+#include "common.h"
+
+namespace {
+
+constexpr int kBlock = 256;
+constexpr int kLoads = 16;  // 16-byte loads per lane per chunk
+
+template <typename T>
+struct Traits;
+template <>
+struct Traits<float> {
+  using V = hpd::f32x4;
+  static constexpr int width = 4;
+};
+template <>
+struct Traits<double> {
+  using V = hpd::f64x2;
+  static constexpr int width = 2;
+};
+
+template <typename T>
+constexpr int64_t chunk_len() {
+  return int64_t(64) * kLoads * Traits<T>::width;
+}
+
+__device__ __forceinline__ float dabs(float x) { return fabsf(x); }
+__device__ __forceinline__ double dabs(double x) { return fabs(x); }
+__device__ __forceinline__ float dldexp(float x, int e) { return ldexpf(x, e); }
+__device__ __forceinline__ double dldexp(double x, int e) { return ldexp(x, e); }
+__device__ __forceinline__ int dexponent(float m) {
+  int e;
+  (void)frexpf(m, &e);
+  return e;
+}
+__device__ __forceinline__ int dexponent(double m) {
+  int e;
+  (void)frexp(m, &e);
+  return e;
+}
+__device__ __forceinline__ float dsqrt(float x) { return sqrtf(x); }
+__device__ __forceinline__ double dsqrt(double x) { return sqrt(x); }
+
+// max|.| that propagates NaN from either side.
+template <typename T>
+__device__ __forceinline__ T nan_max(T a, T b) {
+  return (isnan(a) || a > b) ? a : (isnan(b) ? b : b);
+}
+
+template <typename T>
+__device__ __forceinline__ T wave_nan_max(T v) {
+#pragma unroll
+  for (int o = 32; o > 0; o >>= 1) v = nan_max(v, __shfl_xor(v, o, 64));
+  return v;
+}
+
+// Pair algebra on (k, t): norm^2 = 4^k * t for finite k; k = -inf means 0.
+template <typename T>
+struct Pair {
+  T k, t;
+};
+
+template <typename T>
+__device__ __forceinline__ Pair<T> merge(Pair<T> a, Pair<T> b) {
+  if (isnan(a.k) || isnan(b.k)) return {T(NAN), T(0)};
+  if (isinf(a.k) && a.k > 0) return a;
+  if (isinf(b.k) && b.k > 0) return b;
+  if (isinf(a.k)) return b;  // a is the zero pair
+  if (isinf(b.k)) return a;
+  const T k = a.k > b.k ? a.k : b.k;
+  const T t = dldexp(a.t, 2 * int(a.k - k)) + dldexp(b.t, 2 * int(b.k - k));
+  return {k, t};
+}
+
+template <typename T>
+__device__ __forceinline__ T finish(Pair<T> p) {
+  if (isnan(p.k)) return T(NAN);
+  if (isinf(p.k)) return p.k > 0 ? T(INFINITY) : T(0);
+  return dldexp(dsqrt(p.t), int(p.k));
+}
+
+template <typename T>
+__device__ __forceinline__ Pair<T> wave_merge(Pair<T> p) {
+#pragma unroll
+  for (int o = 32; o > 0; o >>= 1) {
+    Pair<T> q = {__shfl_xor(p.k, o, 64), __shfl_xor(p.t, o, 64)};
+    p = merge(p, q);
+  }
+  return p;
+}
+
+// Reduce registers `v[0..n)` (zeros beyond the valid range) to a wave pair.
+template <typename T, int N>
+__device__ __forceinline__ Pair<T> registers_to_pair(const T (&v)[N]) {
+  T m = T(0);
+#pragma unroll
+  for (int i = 0; i < N; ++i) m = nan_max(dabs(v[i]), m);
+  m = wave_nan_max(m);
+  if (isnan(m)) return {T(NAN), T(0)};
+  if (isinf(m)) return {T(INFINITY), T(0)};
+  if (m == T(0)) return {T(-INFINITY), T(0)};
+  const int e = dexponent(m);
+  T t = T(0);
+#pragma unroll
+  for (int i = 0; i < N; ++i) {
+    const T s = dldexp(v[i], -e);
+    t = t + s * s;
+  }
+  t = hpd::wave_sum(t);
+  return {T(e), t};
+}
+
+// One wave per (row, chunk) of contiguous rows.
+template <typename T, bool kVector>
+__global__ __launch_bounds__(kBlock) void norm_rows_kernel(const T* __restrict__ x, T* __restrict__ out,
+                                                           int64_t outer, int64_t reduced, int64_t chunks,
+                                                           bool final) {
+  using V = typename Traits<T>::V;
+  constexpr int W = Traits<T>::width;
+  constexpr int N = kLoads * W;
+  const int lane = threadIdx.x & 63;
+  const int64_t g = int64_t(blockIdx.x) * (kBlock / 64) + (threadIdx.x >> 6);
+  if (g >= outer * chunks) return;
+  const int64_t o = g / chunks, ch = g - o * chunks;
+  const int64_t begin = ch * chunk_len<T>();
+  const int64_t len = reduced - begin < chunk_len<T>() ? reduced - begin : chunk_len<T>();
+  const T* base = x + o * reduced + begin;
+  T v[N];
+  if (kVector && len == chunk_len<T>()) {
+    const V* bv = reinterpret_cast<const V*>(base);
+    V q[kLoads];
+#pragma unroll
+    for (int i = 0; i < kLoads; ++i) q[i] = __builtin_nontemporal_load(bv + i * 64 + lane);
+#pragma unroll
+    for (int i = 0; i < kLoads; ++i)
+#pragma unroll
+      for (int w = 0; w < W; ++w) v[i * W + w] = q[i][w];
+  } else {
+#pragma unroll
+    for (int i = 0; i < N; ++i) {
+      const int64_t e = int64_t(i) * 64 + lane;
+      v[i] = e < len ? base[e] : T(0);
+    }
+  }
+  const Pair<T> p = registers_to_pair<T, N>(v);
+  if (lane == 0) {
+    if (final) {
+      out[o] = finish(p);
+    } else {
+      out[2 * g] = p.k;
+      out[2 * g + 1] = p.t;
+    }
+  }
+}
+
+// One workgroup per row merges that row's chunk pairs in index order.
+template <typename T>
+__global__ __launch_bounds__(1024) void norm_merge_kernel(const T* __restrict__ pairs, T* __restrict__ out,
+                                                          int64_t chunks) {
+  __shared__ T ks[16], ts[16];
+  const int64_t o = blockIdx.x;
+  const T* row = pairs + 2 * o * chunks;
+  Pair<T> p = {T(-INFINITY), T(0)};
+  for (int64_t c = threadIdx.x; c < chunks; c += blockDim.x) p = merge(p, Pair<T>{row[2 * c], row[2 * c + 1]});
+  p = wave_merge(p);
+  const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
+  if (lane == 0) {
+    ks[wave] = p.k;
+    ts[wave] = p.t;
+  }
+  __syncthreads();
+  if (threadIdx.x == 0) {
+    Pair<T> total = {ks[0], ts[0]};
+    for (int w = 1; w < int(blockDim.x >> 6); ++w) total = merge(total, Pair<T>{ks[w], ts[w]});
+    out[o] = finish(total);
+  }
+}
+
+// Strided reduction axis (inner > 1): one thread per output, two passes.
+template <typename T>
+__global__ __launch_bounds__(kBlock) void norm_cols_kernel(const T* __restrict__ x, T* __restrict__ out,
+                                                           int64_t outer, int64_t reduced, int64_t inner) {
+  const int64_t stride = int64_t(gridDim.x) * blockDim.x;
+  for (int64_t g = int64_t(blockIdx.x) * blockDim.x + threadIdx.x; g < outer * inner; g += stride) {
+    const int64_t o = g / inner, i = g - o * inner;
+    const T* base = x + o * reduced * inner + i;
+    T m = T(0);
+    for (int64_t r = 0; r < reduced; ++r) m = nan_max(dabs(base[r * inner]), m);
+    T result;
+    if (isnan(m) || isinf(m) || m == T(0)) {
+      result = m;
+    } else {
+      const int e = dexponent(m);
+      T t = T(0);
+      for (int64_t r = 0; r < reduced; ++r) {
+        const T s = dldexp(base[r * inner], -e);
+        t = t + s * s;
+      }
+      result = dldexp(dsqrt(t), e);
+    }
+    out[g] = result;
+  }
+}
+
+template <typename T>
+void run_norm(hp_ctx* ctx, const T* x, T* out, int64_t outer, int64_t reduced, int64_t inner) {
+  if (inner > 1) {
+    const int64_t work = outer * inner;
+    int64_t grid = hp::ceil_div(work, kBlock);
+    if (grid > 65536 * 4) grid = 65536 * 4;
+    norm_cols_kernel<T><<<grid, kBlock, 0, ctx->stream>>>(x, out, outer, reduced, inner);
+    hp::check_launch("norm_cols");
+    return;
+  }
+  const int64_t chunks = hp::ceil_div(reduced, chunk_len<T>());
+  const int64_t waves = outer * chunks;
+  const int64_t grid = hp::ceil_div(waves, kBlock / 64);
+  hp::require(grid <= hp::kMaxGrid, "norm input too large for one launch");
+  const bool vector = reinterpret_cast<uintptr_t>(x) % 16 == 0 && (reduced * int64_t(sizeof(T))) % 16 == 0;
+  T* target = out;
+  T* pairs = nullptr;
+  if (chunks > 1) {
+    pairs = static_cast<T*>(hp::scratch_alloc(ctx, size_t(waves) * 2 * sizeof(T)));
+    target = pairs;
+  }
+  if (vector) {
+    norm_rows_kernel<T, true><<<grid, kBlock, 0, ctx->stream>>>(x, target, outer, reduced, chunks, chunks == 1);
+  } else {
+    norm_rows_kernel<T, false><<<grid, kBlock, 0, ctx->stream>>>(x, target, outer, reduced, chunks, chunks == 1);
+  }
+  hp::check_launch("norm_rows");
+  if (chunks > 1) {
+    hp::require(outer <= hp::kMaxGrid, "too many rows for one launch");
+    norm_merge_kernel<T><<<outer, 1024, 0, ctx->stream>>>(pairs, out, chunks);
+    hp::check_launch("norm_merge");
+    hp::scratch_free(ctx, pairs);
+  }
+}
+
+}  // namespace
+
+using hp::guarded;
+using hp::require;
+
+extern "C" {
+
+int hp_norm(hp_ctx* ctx, int dtype, const void* x, void* out, int64_t outer, int64_t reduced, int64_t inner) {
+  return guarded([&] {
+    hp::enter(ctx);
+    require(dtype == HP_F32 || dtype == HP_F64, "norm supports float32 and float64");
+    require(outer >= 0 && reduced >= 0 && inner >= 0, "negative extent");
+    const int64_t count = outer * inner;
+    if (count == 0) return;
+    require(out != nullptr, "null output");
+    if (reduced == 0) {
+      HP_CHECK(hipMemsetAsync(out, 0, size_t(count) * hp::dtype_size(dtype), ctx->stream));
+      return;
+    }
+    require(x != nullptr, "null input");
+    if (dtype == HP_F32) {
+      run_norm<float>(ctx, (const float*)x, (float*)out, outer, reduced, inner);
+    } else {
+      run_norm<double>(ctx, (const double*)x, (double*)out, outer, reduced, inner);
+    }
+  });
+}
+
+}  // extern "C"

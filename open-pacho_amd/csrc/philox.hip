@@ -1,0 +1,220 @@
+// Counter-based Philox4x32-10 generator (Salmon et al., SC11 "Parallel random
+// numbers: as easy as 1, 2, 3"), one counter block per output element in C
+// order, so the stream is independent of launch geometry and call splitting.
+// Stream contract: reference _random.py:19-31 (rounds), :43-45 / :73-77 (unit
+// conversion), :50-56 / :93-102 (transforms), _random_cuda.py:10-28.
+//
+// Throughput is bound by the 32x32->64 integer multiplies (two per round).
+// Each thread produces four consecutive elements for instruction-level
+// parallelism and 16-byte stores. When a wave's 256 counters share their high
+// 32-bit word, that word lives in a scalar register: round 1 then needs one
+// vector multiply (its c2 input is zero) and round 2's c0 product is a scalar
+// multiply, saving 2 of the 20 vector multiplies per element.
+#include "common.h"
+
+namespace {
+
+constexpr uint32_t kM0 = 0xD2511F53u;
+constexpr uint32_t kM1 = 0xCD9E8D57u;
+constexpr uint32_t kW0 = 0x9E3779B9u;
+constexpr uint32_t kW1 = 0xBB67AE85u;
+
+struct Words {
+  uint32_t x0, x1, x2, x3;
+};
+
+__device__ __forceinline__ Words philox10(uint32_t c0, uint32_t c1, uint32_t c2, uint32_t c3, uint32_t k0,
+                                          uint32_t k1) {
+#pragma unroll
+  for (int round = 0; round < 10; ++round) {
+    const uint64_t p0 = uint64_t(c0) * kM0;
+    const uint64_t p1 = uint64_t(c2) * kM1;
+    const uint32_t n0 = uint32_t(p1 >> 32) ^ c1 ^ k0;
+    const uint32_t n2 = uint32_t(p0 >> 32) ^ c3 ^ k1;
+    c0 = n0;
+    c1 = uint32_t(p1);
+    c2 = n2;
+    c3 = uint32_t(p0);
+    k0 += kW0;
+    k1 += kW1;
+  }
+  return {c0, c1, c2, c3};
+}
+
+template <typename T>
+__device__ __forceinline__ T unit(uint32_t a, uint32_t b);
+
+template <>
+__device__ __forceinline__ float unit<float>(uint32_t a, uint32_t) {
+  return float(a >> 8) * 5.9604644775390625e-8f;  // 2^-24, exact
+}
+
+template <>
+__device__ __forceinline__ double unit<double>(uint32_t a, uint32_t b) {
+  return (double(a >> 5) * 67108864.0 + double(b >> 6)) * 1.1102230246251565404236316680908203125e-16;
+}
+
+__device__ __forceinline__ float neg_log1m(float u) { return -log1pf(-u); }
+__device__ __forceinline__ double neg_log1m(double u) { return -log1p(-u); }
+__device__ __forceinline__ float dsqrt(float x) { return sqrtf(x); }
+__device__ __forceinline__ double dsqrt(double x) { return sqrt(x); }
+__device__ __forceinline__ float dcos(float x) { return cosf(x); }
+__device__ __forceinline__ double dcos(double x) { return cos(x); }
+
+template <typename T, int DIST>
+__device__ __forceinline__ T transform(const Words& w, T first, T second, T upper) {
+  const T u = unit<T>(w.x0, w.x1);
+  if (DIST == HP_RANDOM) return u;
+  if (DIST == HP_UNIFORM) {
+    const T value = first + (second - first) * u;
+    return value < first ? first : (value > upper ? upper : value);
+  }
+  const T nl = neg_log1m(u);
+  if (DIST == HP_EXPONENTIAL) return second * nl;
+  const T v = unit<T>(w.x2, w.x3);
+  const T two_pi = T(6.283185307179586476925286766559);
+  return first + second * (dsqrt(T(2) * nl) * dcos(two_pi * v));
+}
+
+template <typename T>
+__device__ __forceinline__ void store4(T* out, int64_t e0, int64_t count, const T (&v)[4]);
+
+template <>
+__device__ __forceinline__ void store4<float>(float* out, int64_t e0, int64_t count, const float (&v)[4]) {
+  if (e0 + 3 < count) {
+    hpd::f32x4 q = {v[0], v[1], v[2], v[3]};
+    *reinterpret_cast<hpd::f32x4*>(out + e0) = q;
+  } else {
+    for (int j = 0; j < 4; ++j)
+      if (e0 + j < count) out[e0 + j] = v[j];
+  }
+}
+
+template <>
+__device__ __forceinline__ void store4<double>(double* out, int64_t e0, int64_t count, const double (&v)[4]) {
+  if (e0 + 3 < count) {
+    hpd::f64x2 a = {v[0], v[1]}, b = {v[2], v[3]};
+    reinterpret_cast<hpd::f64x2*>(out + e0)[0] = a;
+    reinterpret_cast<hpd::f64x2*>(out + e0)[1] = b;
+  } else {
+    for (int j = 0; j < 4; ++j)
+      if (e0 + j < count) out[e0 + j] = v[j];
+  }
+}
+
+constexpr int kBlock = 256;
+constexpr int kPerThread = 4;
+
+template <typename T, int DIST>
+__global__ __launch_bounds__(kBlock) void philox_kernel(T* __restrict__ out, int64_t count, uint32_t k0,
+                                                        uint32_t k1, uint64_t start, T first, T second,
+                                                        T upper) {
+  const int64_t block_first = int64_t(blockIdx.x) * (kBlock * kPerThread);
+  const uint32_t wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
+  const uint64_t wave_first = start + uint64_t(block_first) + uint64_t(wave) * (64 * kPerThread);
+  const uint64_t wave_last = wave_first + (64 * kPerThread - 1);
+  const int64_t e0 = block_first + int64_t(threadIdx.x) * kPerThread;
+  if (e0 >= count) return;
+  T values[4];
+  if (uint32_t(wave_first >> 32) == uint32_t(wave_last >> 32)) {
+    // Wave-uniform high word: no carry inside this wave's counters.
+    const uint32_t hi = uint32_t(wave_first >> 32);
+    const uint32_t lo0 = uint32_t(start) + uint32_t(e0);
+#pragma unroll
+    for (int j = 0; j < kPerThread; ++j) {
+      const Words w = philox10(lo0 + uint32_t(j), hi, 0u, 0u, k0, k1);
+      values[j] = transform<T, DIST>(w, first, second, upper);
+    }
+  } else {
+#pragma unroll
+    for (int j = 0; j < kPerThread; ++j) {
+      const uint64_t counter = start + uint64_t(e0 + j);
+      const Words w = philox10(uint32_t(counter), uint32_t(counter >> 32), 0u, 0u, k0, k1);
+      values[j] = transform<T, DIST>(w, first, second, upper);
+    }
+  }
+  store4<T>(out, e0, count, values);
+}
+
+__global__ __launch_bounds__(kBlock) void philox_words_kernel(uint32_t* __restrict__ out, int64_t count,
+                                                              uint32_t k0, uint32_t k1, uint64_t start) {
+  const int64_t i = int64_t(blockIdx.x) * kBlock + threadIdx.x;
+  if (i >= count) return;
+  const uint64_t counter = start + uint64_t(i);
+  const Words w = philox10(uint32_t(counter), uint32_t(counter >> 32), 0u, 0u, k0, k1);
+  uint4 q;
+  q.x = w.x0;
+  q.y = w.x1;
+  q.z = w.x2;
+  q.w = w.x3;
+  reinterpret_cast<uint4*>(out)[i] = q;
+}
+
+template <typename T>
+void launch(hp_ctx* ctx, int dist, T* out, int64_t count, uint32_t k0, uint32_t k1, uint64_t start, T first,
+            T second, T upper) {
+  const int64_t grid = hp::ceil_div(count, kBlock * kPerThread);
+  hp::require(grid <= hp::kMaxGrid, "random output too large for one launch");
+  switch (dist) {
+    case HP_RANDOM:
+      philox_kernel<T, HP_RANDOM><<<grid, kBlock, 0, ctx->stream>>>(out, count, k0, k1, start, first, second, upper);
+      break;
+    case HP_UNIFORM:
+      philox_kernel<T, HP_UNIFORM><<<grid, kBlock, 0, ctx->stream>>>(out, count, k0, k1, start, first, second, upper);
+      break;
+    case HP_NORMAL:
+      philox_kernel<T, HP_NORMAL><<<grid, kBlock, 0, ctx->stream>>>(out, count, k0, k1, start, first, second, upper);
+      break;
+    case HP_EXPONENTIAL:
+      philox_kernel<T, HP_EXPONENTIAL><<<grid, kBlock, 0, ctx->stream>>>(out, count, k0, k1, start, first, second, upper);
+      break;
+    default:
+      hp::fail(HP_E_INVALID, "unknown distribution code " + std::to_string(dist));
+  }
+  hp::check_launch("philox");
+}
+
+}  // namespace
+
+using hp::guarded;
+using hp::require;
+
+extern "C" {
+
+int hp_philox(hp_ctx* ctx, int dtype, int dist, void* out, int64_t count, uint64_t seed, uint64_t start,
+              double first, double second, double upper) {
+  return guarded([&] {
+    hp::enter(ctx);
+    require(count >= 0, "negative count");
+    require(dtype == HP_F32 || dtype == HP_F64, "random generation requires float32 or float64");
+    require(dist >= HP_RANDOM && dist <= HP_EXPONENTIAL, "unknown distribution code");
+    // The counter range [start, start + count) must fit in 64 bits.
+    require(count == 0 || uint64_t(count) - 1 <= ~start, "Philox counter range exceeds 2^64");
+    if (count == 0) return;
+    require(out != nullptr && reinterpret_cast<uintptr_t>(out) % 16 == 0,
+            "random output must be a 16-byte aligned device buffer");
+    const uint32_t k0 = uint32_t(seed), k1 = uint32_t(seed >> 32);
+    if (dtype == HP_F32) {
+      launch<float>(ctx, dist, static_cast<float*>(out), count, k0, k1, start, float(first), float(second),
+                    float(upper));
+    } else {
+      launch<double>(ctx, dist, static_cast<double*>(out), count, k0, k1, start, first, second, upper);
+    }
+  });
+}
+
+int hp_philox_words(hp_ctx* ctx, uint32_t* out, int64_t count, uint64_t seed, uint64_t start) {
+  return guarded([&] {
+    hp::enter(ctx);
+    require(count >= 0, "negative count");
+    require(count == 0 || uint64_t(count) - 1 <= ~start, "Philox counter range exceeds 2^64");
+    if (count == 0) return;
+    require(out != nullptr && reinterpret_cast<uintptr_t>(out) % 16 == 0, "output must be 16-byte aligned");
+    const int64_t grid = hp::ceil_div(count, kBlock);
+    require(grid <= hp::kMaxGrid, "output too large for one launch");
+    philox_words_kernel<<<grid, kBlock, 0, ctx->stream>>>(out, count, uint32_t(seed), uint32_t(seed >> 32), start);
+    hp::check_launch("philox_words");
+  });
+}
+
+}  // extern "C"

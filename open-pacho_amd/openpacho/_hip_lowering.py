@@ -1,0 +1,361 @@
+"""hipRTC lowering of elementwise groups and mapped reductions for ``hip``.
+
+The compiler owns grouping; this module turns one group into HIP source that
+hp_rtc_compile builds for gfx950 with contraction off. Payloads hold source
+text and launch geometry only, never runtime arrays or scalar values, so a
+cached plan rebinds fresh operands on every call.
+
+Numerics follow the reference lowering (_cuda_lowering.py:13-41): every node
+converts each operand to its resolved dtype before the operation and rounds
+its result to the node dtype, so a fused chain rounds exactly like the eager
+sequence of NumPy-typed operations. Booleans are stored as one byte.
+Integer add/subtract/multiply/negate wrap modulo 2^bits as in NumPy.
+Mapped reductions use the extrema contract of the reduction kernels
+(NaN propagates, min prefers -0, max prefers +0).
+"""
+
+from math import prod
+
+import numpy as np
+
+from ._array import ndarray
+
+_CTYPE = {
+    np.dtype("bool"): "unsigned char",
+    np.dtype("int32"): "int",
+    np.dtype("int64"): "long long",
+    np.dtype("uint32"): "unsigned int",
+    np.dtype("uint64"): "unsigned long long",
+    np.dtype("float32"): "float",
+    np.dtype("float64"): "double",
+}
+_UNSIGNED = {np.dtype("int32"): "unsigned int", np.dtype("int64"): "unsigned long long"}
+
+BLOCK = 256
+ELEMENTS_PER_THREAD = 4
+REDUCE_CHUNK = 8192
+
+_PRELUDE = r"""
+template <typename T> __device__ __forceinline__ T pacho_min(T a, T b) { return a < b ? a : b; }
+template <typename T> __device__ __forceinline__ T pacho_max(T a, T b) { return a > b ? a : b; }
+__device__ __forceinline__ float pacho_min(float a, float b) {
+  if (isnan(a)) return a; if (isnan(b)) return b;
+  if (a == 0.0f && b == 0.0f) return signbit(a) ? a : b;
+  return a < b ? a : b;
+}
+__device__ __forceinline__ float pacho_max(float a, float b) {
+  if (isnan(a)) return a; if (isnan(b)) return b;
+  if (a == 0.0f && b == 0.0f) return signbit(a) ? b : a;
+  return a > b ? a : b;
+}
+__device__ __forceinline__ double pacho_min(double a, double b) {
+  if (isnan(a)) return a; if (isnan(b)) return b;
+  if (a == 0.0 && b == 0.0) return signbit(a) ? a : b;
+  return a < b ? a : b;
+}
+__device__ __forceinline__ double pacho_max(double a, double b) {
+  if (isnan(a)) return a; if (isnan(b)) return b;
+  if (a == 0.0 && b == 0.0) return signbit(a) ? b : a;
+  return a > b ? a : b;
+}
+"""
+
+
+def ctype(dtype):
+    return _CTYPE[np.dtype(dtype)]
+
+
+def _operation(op, resolved, out_dtype):
+    """C expression of ``op`` over operands ``a``, ``b``, ``c`` of the resolved dtypes."""
+    kind = resolved[0].kind if resolved else "f"
+    dt = resolved[0] if resolved else out_dtype
+    wrap = dt in _UNSIGNED and op in ("add", "subtract", "multiply", "negative")
+    if wrap:
+        u, t = _UNSIGNED[dt], ctype(dt)
+        return {
+            "add": f"({t})(({u})a + ({u})b)",
+            "subtract": f"({t})(({u})a - ({u})b)",
+            "multiply": f"({t})(({u})a * ({u})b)",
+            "negative": f"({t})(({u})0 - ({u})a)",
+        }[op]
+    if op == "absolute":
+        if kind == "f":
+            return "fabs(a)"
+        if kind == "i":
+            u, t = _UNSIGNED[dt], ctype(dt)
+            return f"(a < 0 ? ({t})(({u})0 - ({u})a) : a)"
+        return "a"
+    if op == "isfinite":
+        return "isfinite(a)" if kind == "f" else "1"
+    table = {
+        "add": "a + b",
+        "subtract": "a - b",
+        "multiply": "a * b",
+        "true_divide": "a / b",
+        "divide": "a / b",
+        "power": "pow(a, b)",
+        "negative": "-a",
+        "positive": "a",
+        "sqrt": "sqrt(a)",
+        "exp": "exp(a)",
+        "log": "log(a)",
+        "sin": "sin(a)",
+        "cos": "cos(a)",
+        "tanh": "tanh(a)",
+        "equal": "a == b",
+        "not_equal": "a != b",
+        "less": "a < b",
+        "less_equal": "a <= b",
+        "greater": "a > b",
+        "greater_equal": "a >= b",
+        "cast": "a",
+        "where": "(a != 0) ? b : c",
+    }
+    if op not in table:
+        raise NotImplementedError(f"hip lowering has no rule for {op}")
+    return table[op]
+
+
+def _broadcast_offset(root_shape, leaf_shape, var):
+    """Element offset of ``leaf`` (right-aligned broadcast) at flat root index ``var``."""
+    if tuple(leaf_shape) == tuple(root_shape):
+        return var
+    lead = len(root_shape) - len(leaf_shape)
+    terms = []
+    for axis, extent in enumerate(leaf_shape):
+        if extent == 1:
+            continue
+        outer = prod(root_shape[lead + axis + 1 :])
+        inner = prod(leaf_shape[axis + 1 :])
+        terms.append(f"(({var} / {max(1, outer)}LL) % {extent}LL) * {inner}LL")
+    return " + ".join(terms) or "0LL"
+
+
+class _Leaf:
+    __slots__ = ("scalar", "dtype", "shape")
+
+    def __init__(self, scalar, dtype, shape):
+        self.scalar, self.dtype, self.shape = scalar, np.dtype(dtype), tuple(shape)
+
+
+def _body(root_shape, leaves, nodes, var="i"):
+    """Source lines computing each node; returns (params, lines, result symbol).
+
+    ``leaves`` is a list of _Leaf; ``nodes`` a list of (op, input refs,
+    resolved dtypes, out dtype) where refs index leaves (0..L-1) then nodes.
+    """
+    params, lines, names = [], [], []
+    for k, leaf in enumerate(leaves):
+        t = ctype(leaf.dtype)
+        if leaf.scalar:
+            params.append(f"{t} x{k}")
+            lines.append(f"const {t} v{k} = x{k};")
+        else:
+            params.append(f"const {t}* __restrict__ x{k}")
+            lines.append(f"const {t} v{k} = x{k}[{_broadcast_offset(root_shape, leaf.shape, var)}];")
+        names.append(f"v{k}")
+    for j, (op, refs, resolved, out_dtype) in enumerate(nodes):
+        symbol = f"v{len(leaves) + j}"
+        lines.append(f"{ctype(out_dtype)} {symbol};")
+        lines.append("{")
+        for label, ref, dt in zip("abc", refs, resolved):
+            source = names[ref]
+            if dt.kind == "b":
+                source = f"({source} != 0)"
+            lines.append(f"  const {ctype(dt)} {label} = ({ctype(dt)})({source});")
+        expression = _operation(op, resolved, out_dtype)
+        if out_dtype.kind == "b":
+            expression = f"(({expression}) != 0)"
+        lines.append(f"  {symbol} = ({ctype(out_dtype)})({expression});")
+        lines.append("}")
+        names.append(symbol)
+    return params, lines, names[-1]
+
+
+def elementwise_source(root_shape, leaves, nodes, out_dtype):
+    count = prod(root_shape)
+    params, lines, result = _body(root_shape, leaves, nodes)
+    params.append(f"{ctype(out_dtype)}* __restrict__ out")
+    body = "\n      ".join(lines)
+    span = BLOCK * ELEMENTS_PER_THREAD
+    source = f"""{_PRELUDE}
+extern "C" __global__ __launch_bounds__({BLOCK}) void pacho_elementwise({", ".join(params)}) {{
+  const long long base = (long long)blockIdx.x * {span}LL + threadIdx.x;
+#pragma unroll
+  for (int u = 0; u < {ELEMENTS_PER_THREAD}; ++u) {{
+    const long long i = base + (long long)u * {BLOCK}LL;
+    if (i < {count}LL) {{
+      {body}
+      out[i] = {result};
+    }}
+  }}
+}}
+"""
+    grid = max(1, -(-count // span))
+    return source, grid
+
+
+def _identity(operation, dtype):
+    t = ctype(dtype)
+    if operation == "sum":
+        return f"({t})0"
+    if dtype.kind == "b":
+        return "1" if operation == "min" else "0"
+    if dtype.kind == "f":
+        huge = "__builtin_huge_valf()" if dtype.itemsize == 4 else "__builtin_huge_val()"
+        return f"({t})(-{huge})" if operation == "max" else f"({t})({huge})"
+    info = np.iinfo(dtype)
+    value = info.max if operation == "min" else info.min
+    if dtype.kind == "i" and value == info.min:
+        return f"(({t})({value + 1}LL) - ({t})1)"
+    suffix = "ULL" if dtype.kind == "u" else "LL"
+    return f"({t})({value}{suffix})"
+
+
+def _combine(operation, dtype, left, right):
+    if operation == "sum":
+        return f"({left}) + ({right})"
+    if dtype.kind == "b":
+        op = "&&" if operation == "min" else "||"
+        return f"(unsigned char)((({left}) != 0) {op} (({right}) != 0))"
+    return f"pacho_{operation}({left}, {right})"
+
+
+def _reduction_index(shape, axes):
+    """Index of element (o, r) of ``shape`` with ``axes`` reduced, plus counts."""
+    out_dims = [d for i, d in enumerate(shape) if i not in axes]
+    red_dims = [shape[i] for i in axes]
+    terms, oi, ri = [], 0, 0
+    for axis, extent in enumerate(shape):
+        stride = prod(shape[axis + 1 :])
+        if axis in axes:
+            step = prod(red_dims[ri + 1 :])
+            terms.append(f"((r / {max(1, step)}LL) % {max(1, extent)}LL) * {stride}LL")
+            ri += 1
+        else:
+            step = prod(out_dims[oi + 1 :])
+            terms.append(f"((o / {max(1, step)}LL) % {max(1, extent)}LL) * {stride}LL")
+            oi += 1
+    return " + ".join(terms) or "0LL", prod(out_dims), prod(red_dims)
+
+
+def map_reduce_source(mapped_shape, axes, leaves, nodes, operation, acc_dtype):
+    index, count, reduced = _reduction_index(mapped_shape, axes)
+    chunks = max(1, -(-reduced // REDUCE_CHUNK))
+    if nodes:
+        params, lines, result = _body(mapped_shape, leaves, nodes)
+    else:  # reduction of a materialised array: the single leaf is the value
+        params, lines, result = _body(mapped_shape, leaves, [])
+    acc = ctype(acc_dtype)
+    value = f"({result} != 0)" if (nodes and nodes[-1][3].kind == "b") else result
+    params.append(f"{acc}* __restrict__ out")
+    body = "\n      ".join(lines)
+    waves = BLOCK // 64
+    source = f"""{_PRELUDE}
+extern "C" __global__ __launch_bounds__({BLOCK}) void pacho_map_reduce({", ".join(params)}) {{
+  __shared__ {acc} partial[{waves}];
+  const long long g = blockIdx.x;
+  const long long o = g / {chunks}LL, chunk = g % {chunks}LL;
+  const long long begin = chunk * {REDUCE_CHUNK}LL;
+  const long long end = begin + {REDUCE_CHUNK}LL < {reduced}LL ? begin + {REDUCE_CHUNK}LL : {reduced}LL;
+  {acc} acc = {_identity(operation, acc_dtype)};
+  for (long long r = begin + threadIdx.x; r < end; r += {BLOCK}LL) {{
+    const long long i = {index};
+    {{
+      {body}
+      acc = {_combine(operation, acc_dtype, "acc", f"({acc})({value})")};
+    }}
+  }}
+#pragma unroll
+  for (int offset = 1; offset < 64; offset <<= 1) {{
+    const {acc} other = __shfl_xor(acc, offset, 64);
+    acc = {_combine(operation, acc_dtype, "acc", "other")};
+  }}
+  if ((threadIdx.x & 63) == 0) partial[threadIdx.x >> 6] = acc;
+  __syncthreads();
+  if (threadIdx.x == 0) {{
+    {acc} total = partial[0];
+    for (int w = 1; w < {waves}; ++w) total = {_combine(operation, acc_dtype, "total", "partial[w]")};
+    out[g] = total;
+  }}
+}}
+"""
+    return source, count, chunks
+
+
+def _leaf_of(node):
+    return _Leaf(node.op == "scalar", node.dtype, node.shape)
+
+
+def _graph(group, leaves):
+    position = {id(leaf): k for k, leaf in enumerate(leaves)}
+    nodes = []
+    for j, node in enumerate(group):
+        position[id(node)] = len(leaves) + j
+        refs = [position[id(child)] for child in node.inputs]
+        nodes.append((node.op, refs, tuple(np.dtype(d) for d in node.resolved), np.dtype(node.dtype)))
+    return [_leaf_of(leaf) for leaf in leaves], nodes
+
+
+class HIPLowering:
+    """Lowering protocol of the compiler (prepare/run for fused and map_reduce)."""
+
+    def __init__(self, backend):
+        self.backend = backend
+
+    def can_residual_matvec(self, matrix, vector, rhs, node):
+        # The GEMV residual epilogue is not fused on this backend; the
+        # product and the subtraction stay separate steps.
+        return False
+
+    def can_reduce_materialized(self, node):
+        return (
+            node.dtype.kind == "f"
+            and node.dtype.itemsize == 4
+            and node.attrs.get("operation") in ("min", "max")
+        )
+
+    def prepare_fused(self, node, group, leaves):
+        specs, nodes = _graph(group, leaves)
+        source, grid = elementwise_source(node.shape, specs, nodes, np.dtype(node.dtype))
+        return tuple(leaves), (source, grid)
+
+    def run_fused(self, node, payload, arguments, operands):
+        source, grid = payload
+        out = self.backend.empty(node.shape, node.dtype)
+        self.backend._launch(source, "pacho_elementwise", grid, operands, out)
+        return out
+
+    def prepare_map_reduce(self, node, group, leaves):
+        operation = node.attrs.get("operation", "sum")
+        if node.dtype.kind == "b" and operation == "sum":
+            raise NotImplementedError("Boolean sum requires a numeric accumulator dtype")
+        mapped = node.inputs[0]
+        if prod(mapped.shape) > 2**31 - 1:
+            raise ValueError("Array exceeds GPU indexing limits")
+        specs, nodes = _graph(group, leaves)
+        source, count, chunks = map_reduce_source(
+            mapped.shape, tuple(node.attrs["axes"]), specs, nodes, operation, np.dtype(node.dtype)
+        )
+        return tuple(leaves), (source, count, chunks)
+
+    def run_map_reduce(self, node, payload, arguments, operands):
+        source, count, chunks = payload
+        out = self.backend.empty((count, chunks), node.dtype)
+        self.backend._launch(source, "pacho_map_reduce", count * chunks, operands, out)
+        if chunks == 1:
+            return out
+        partial = ndarray._wrap(out, (count, chunks), node.dtype, self.backend)
+        options = {"operation": node.attrs["operation"]} if "operation" in node.attrs else {}
+        return self.backend.reduce(partial, (1,), False, node.dtype, **options)
+
+
+def eager_source(name, args, shape, dtype):
+    """Source of one eager elementwise operation (a one-node fused group)."""
+    leaves = [_Leaf(getattr(a, "_host_scalar", False), a.dtype, a.shape) for a in args]
+    dtype = np.dtype(dtype)
+    resolved = tuple(np.dtype(a.dtype) for a in args)
+    if name == "cast":
+        resolved = (resolved[0],)
+    nodes = [(name, list(range(len(args))), resolved, dtype)]
+    return elementwise_source(tuple(shape), leaves, nodes, dtype)

@@ -1,0 +1,276 @@
+"""GPU parity of the MFMA GEMM (hp_gemm, hp_pad_copy) against fp64/exact oracles.
+
+Cases follow reference tests/test_cuda.py:280-441 (vector/irregular/empty/K=0
+products, NaN/Inf-poisoned destinations, batched broadcasting),
+tests/test_padding.py:374-527 (padded plans, special values, signed zeros)
+and BASELINE.json config 4 (8192^3 fp32, 4096^3 fp64, 4097x3001x2049 padded,
+64x(512x1024)@(1024x768)). The error bar: hip error against the exact/fp64
+oracle <= 2x the error of the reference kernel's sequential-K order
+(oracle.kernels.gemm_sequential) on the same sampled outputs.
+"""
+
+import numpy as np
+import pytest
+
+import openpacho as p
+from oracle import exact, kernels
+from oracle import padding as pad_oracle
+
+pytestmark = pytest.mark.gpu
+
+MATMUL_CASES = (
+    ("vector", np.asarray([1.25, -2.0, 0.5, 3.0, -1.0, 2.5, 4.0]), np.asarray([-2.0, 3.0, 1.5, -0.5, 2.0, 0.25, -1.0])),
+    ("gemv", np.arange(15, dtype=np.float64).reshape(3, 5) / 11, np.asarray([1.0, -2.0, 0.5, 3.0, -1.5])),
+    ("vecmat", np.asarray([1.0, -2.0, 0.5, 3.0, -1.5]), np.arange(20, dtype=np.float64).reshape(5, 4) / 13),
+    ("irregular_gemm", np.arange(35, dtype=np.float64).reshape(5, 7) / 17, np.arange(21, dtype=np.float64).reshape(7, 3) / 19),
+    ("odd_tile_gemm", np.arange(33 * 17, dtype=np.float64).reshape(33, 17) / 101, np.arange(17 * 65, dtype=np.float64).reshape(17, 65) / 103),
+    ("large_odd_gemm", np.arange(65 * 63, dtype=np.float64).reshape(65, 63) / 107, np.arange(63 * 97, dtype=np.float64).reshape(63, 97) / 109),
+)
+
+
+def _tol(dtype):
+    return (3e-5, 3e-6) if np.dtype(dtype) == np.float32 else (2e-11, 2e-12)
+
+
+def test_vector_and_irregular_products(hip):
+    for dtype in (np.float32, np.float64):
+        for name, left, right in MATMUL_CASES:
+            left, right = left.astype(dtype), right.astype(dtype)
+            actual = p.matmul(p.asarray(left, backend=hip), p.asarray(right, backend=hip))
+            rtol, atol = _tol(dtype)
+            np.testing.assert_allclose(p.asnumpy(actual), np.matmul(left, right), rtol=rtol, atol=atol, err_msg=name)
+            assert p.asnumpy(actual).dtype == dtype
+
+
+@pytest.mark.parametrize("left_shape,right_shape", [((0, 5), (5, 3)), ((2, 0), (0, 3)), ((1, 0), (0, 7)), ((4, 3), (3, 0)), ((0,), (0,))])
+def test_empty_and_k0_products(hip, left_shape, right_shape):
+    for dtype in (np.float32, np.float64):
+        left, right = np.zeros(left_shape, dtype), np.zeros(right_shape, dtype)
+        actual = p.asnumpy(p.matmul(p.asarray(left, backend=hip), p.asarray(right, backend=hip)))
+        np.testing.assert_array_equal(actual, np.matmul(left, right))
+
+
+def _poisoned(backend, left, right, dtype, poison, monkeypatch):
+    left, right = left.astype(dtype), right.astype(dtype)
+    expected = np.matmul(left, right)
+    a, b = p.asarray(left, backend=backend), p.asarray(right, backend=backend)
+    destination = p.full(expected.shape, poison, dtype=dtype, backend=backend)
+    original = backend.empty
+
+    def poisoned_empty(shape, requested):
+        if tuple(shape) == expected.shape and np.dtype(requested) == np.dtype(dtype):
+            return destination._data
+        return original(shape, requested)
+
+    monkeypatch.setattr(backend, "empty", poisoned_empty)
+    actual = p.matmul(a, b)
+    monkeypatch.undo()
+    assert actual._data is destination._data
+    return actual, expected
+
+
+def test_products_overwrite_nan_and_inf_destinations(hip, monkeypatch):
+    for dtype in (np.float32, np.float64):
+        for poison in (np.nan, np.inf):
+            for name, left, right in MATMUL_CASES[:4]:
+                actual, expected = _poisoned(hip, left, right, dtype, poison, monkeypatch)
+                rtol, atol = _tol(dtype)
+                np.testing.assert_allclose(p.asnumpy(actual), expected, rtol=rtol, atol=atol, err_msg=name)
+
+
+@pytest.mark.parametrize("dtype", [np.float32, np.float64])
+@pytest.mark.parametrize(
+    "shapes",
+    [
+        ((3, 33, 17), (3, 17, 65)),
+        ((2, 1, 33, 17), (1, 3, 17, 65)),
+        ((2, 5, 7), (7, 3)),
+        ((5, 7), (2, 7, 3)),
+        ((2, 5, 7), (7,)),
+        ((7,), (2, 7, 3)),
+        ((2, 5, 0), (2, 0, 3)),
+        ((0, 5, 7), (1, 7, 3)),
+        ((2, 3, 1, 40, 24), (3, 4, 24, 72)),
+    ],
+)
+def test_batched_broadcast_products(hip, dtype, shapes):
+    rng = np.random.default_rng(830)
+    left, right = (rng.normal(size=s).astype(dtype) for s in shapes)
+    a, b = p.asarray(left, backend=hip), p.asarray(right, backend=hip)
+    operation = p.compile(lambda x, y: x @ y)
+    rtol, atol = (3e-5, 3e-5) if dtype == np.float32 else (2e-11, 2e-12)
+    for result in (a @ b, operation(a, b)):
+        np.testing.assert_allclose(p.asnumpy(result), left @ right, rtol=rtol, atol=atol)
+
+
+@pytest.mark.parametrize("dtype", [np.float32, np.float64])
+@pytest.mark.parametrize(
+    "m,n,k",
+    [
+        (256, 128, 16),  # one interior tile
+        (512, 256, 64),  # interior, several tiles and slices
+        (257, 129, 17),  # every edge guarded, scalar loads (K odd)
+        (300, 200, 100),  # guarded vector loads
+        (1, 1, 1),
+        (31, 33, 4099),  # long K, partial tiles
+        (640, 384, 48),
+    ],
+)
+def test_kernel_modes_against_float64(hip, dtype, m, n, k):
+    rng = np.random.default_rng(m * 7 + n * 3 + k)
+    a = rng.uniform(-1, 1, (m, k)).astype(dtype)
+    b = rng.uniform(-1, 1, (k, n)).astype(dtype)
+    got = p.asnumpy(p.asarray(a, backend=hip) @ p.asarray(b, backend=hip))
+    want = a.astype(np.float64) @ b.astype(np.float64)
+    scale = np.abs(a).astype(np.float64) @ np.abs(b).astype(np.float64)
+    bound = (4e-7 if dtype == np.float32 else 8e-16) * np.sqrt(k) * 4
+    assert np.all(np.abs(got - want) <= bound * scale + 1e-30)
+
+
+def _sampled_error_ratio(a, b, got, samples, seed):
+    """(hip error, reference-order error) over sampled outputs, exact oracle."""
+    rng = np.random.default_rng(seed)
+    rows = rng.integers(0, a.shape[0], samples)
+    cols = rng.integers(0, b.shape[1], samples)
+    ref = kernels.gemm_sequential(a, b, rows, cols)
+    hip_err, ref_err = [], []
+    for i, (r, c) in enumerate(zip(rows, cols)):
+        truth = exact.exact_dot(a[r, :], b[:, c])
+        scale = float(exact.exact_dot(np.abs(a[r, :]), np.abs(b[:, c])))
+        hip_err.append(abs(float(got[i] if got.ndim == 1 else got[r, c]) - float(truth)) / scale)
+        ref_err.append(abs(float(ref[i]) - float(truth)) / scale)
+    return float(np.sqrt(np.mean(np.square(hip_err)))), float(np.sqrt(np.mean(np.square(ref_err))))
+
+
+def test_config1_shape_1024_cubed_within_2x_reference_kernel_error(hip):
+    rng = np.random.default_rng(0)
+    a = rng.uniform(-1, 1, (1024, 1024)).astype(np.float32)
+    b = rng.uniform(-1, 1, (1024, 1024)).astype(np.float32)
+    got = p.asnumpy(p.asarray(a, backend=hip) @ p.asarray(b, backend=hip))
+    hip_err, ref_err = _sampled_error_ratio(a, b, got, 256, 5)
+    assert hip_err <= 2 * ref_err
+    want = a.astype(np.float64) @ b.astype(np.float64)
+    assert np.linalg.norm(got - want) / np.linalg.norm(want) < 1e-6
+
+
+def test_config4_fp32_8192_cubed(hip):
+    n = 8192
+    rng = np.random.default_rng(3)
+    a = rng.uniform(-1, 1, (n, n)).astype(np.float32)
+    b = rng.uniform(-1, 1, (n, n)).astype(np.float32)
+    c = p.asarray(a, backend=hip) @ p.asarray(b, backend=hip)
+    rows = np.array([0, 1, 4095, 8191])
+    got_rows = p.asnumpy(c[4095:4096])  # gather of one row
+    assert got_rows.shape == (1, n)
+    full = p.asnumpy(c)
+    want = exact.float64_matmul_rows(a, b, rows)
+    np.testing.assert_allclose(full[rows], want, rtol=0, atol=5e-4)
+    np.testing.assert_array_equal(full[4095], got_rows[0])
+    hip_err, ref_err = _sampled_error_ratio(a, b, full, 48, 6)
+    assert hip_err <= 2 * ref_err
+
+
+def test_config4_fp64_4096_cubed(hip):
+    n = 4096
+    rng = np.random.default_rng(3)
+    a = rng.uniform(-1, 1, (n, n))
+    b = rng.uniform(-1, 1, (n, n))
+    full = p.asnumpy(p.asarray(a, backend=hip) @ p.asarray(b, backend=hip))
+    hip_err, ref_err = _sampled_error_ratio(a, b, full, 48, 7)
+    assert hip_err <= 2 * ref_err
+    np.testing.assert_allclose(full[[0, 2047, 4095]], a[[0, 2047, 4095]] @ b, rtol=0, atol=1e-11)
+
+
+def test_config4_padded_odd_shape(hip):
+    m, k, n = 4097, 3001, 2049
+    rng = np.random.default_rng(3)
+    a = rng.uniform(-1, 1, (m, k)).astype(np.float32)
+    b = rng.uniform(-1, 1, (k, n)).astype(np.float32)
+    A, B = p.asarray(a, backend=hip), p.asarray(b, backend=hip)
+    compiled = p.compile(lambda x, y: p.matmul(x, y), padding=True)
+    step = [s for s in compiled.explain(A, B)["steps"] if s["kind"] == "padded_matmul"]
+    assert len(step) == 1
+    info = step[0]["padding"]
+    expected = pad_oracle.plan((m, k), (k, n))
+    assert info["padded_input_shapes"] == expected["padded_input_shapes"]
+    assert info["scratch_bytes"] == expected["scratch_bytes"] == 109_039_616
+    assert info["copy_dispatches"] == 3 and info["alignment"] == (32, 16, 32)
+    for result in (p.matmul(A, B, padding=True), compiled(A, B)):
+        got = p.asnumpy(result)
+        assert got.shape == (m, n)
+        rows = np.array([0, 2048, 4096])
+        np.testing.assert_allclose(got[rows], exact.float64_matmul_rows(a, b, rows), rtol=0, atol=5e-4)
+        hip_err, ref_err = _sampled_error_ratio(a, b, got, 32, 8)
+        assert hip_err <= 2 * ref_err
+    np.testing.assert_array_equal(p.asnumpy(A), a)
+
+
+def test_config4_batched_broadcast(hip):
+    rng = np.random.default_rng(3)
+    a = rng.uniform(-1, 1, (64, 512, 1024)).astype(np.float32)
+    b = rng.uniform(-1, 1, (1024, 768)).astype(np.float32)
+    got = p.asnumpy(p.asarray(a, backend=hip) @ p.asarray(b, backend=hip))
+    assert got.shape == (64, 512, 768)
+    for batch in (0, 31, 63):
+        want = a[batch].astype(np.float64) @ b.astype(np.float64)
+        np.testing.assert_allclose(got[batch], want, rtol=0, atol=2e-4)
+
+
+@pytest.mark.parametrize("shapes", [((33, 17), (17, 65)), ((65, 47), (47, 67)), ((64, 32), (32, 96)), ((2, 1, 33, 17), (1, 3, 17, 65))])
+def test_padding_rounds_to_tiles_and_preserves_logical_results(hip, shapes):
+    rng = np.random.default_rng(8301)
+    left, right = (rng.uniform(-0.5, 0.5, size=s).astype(np.float32) for s in shapes)
+    a, b = p.asarray(left, backend=hip), p.asarray(right, backend=hip)
+    compiled = p.compile(lambda x, y: p.matmul(x, y), padding=True)
+    details = compiled.explain(a, b)
+    step = [s for s in details["steps"] if s["kind"] == "padded_matmul"][0]["padding"]
+    plan = pad_oracle.plan(*shapes)
+    assert tuple(step["padded_input_shapes"]) == plan["padded_input_shapes"]
+    assert tuple(step["padded_output_shape"]) == plan["padded_output_shape"]
+    assert step["scratch_bytes"] == plan["scratch_bytes"]
+    expected = left.astype(np.float64) @ right.astype(np.float64)
+    prepared = compiled.prepare(a, b)
+    first = compiled(a, b)
+    for result in (p.matmul(a, b, padding=True), first, prepared(a, b)):
+        np.testing.assert_allclose(p.asnumpy(result), expected, rtol=5e-4, atol=5e-4)
+    snapshot = p.asnumpy(first)
+    again = prepared(a, b)
+    assert first._data is not again._data
+    np.testing.assert_array_equal(p.asnumpy(a), left)
+    np.testing.assert_array_equal(p.asnumpy(first), snapshot)
+    changed = prepared(p.asarray(left + np.float32(0.25), backend=hip), p.asarray(right - np.float32(0.125), backend=hip))
+    want = (left + np.float32(0.25)).astype(np.float64) @ (right - np.float32(0.125)).astype(np.float64)
+    np.testing.assert_allclose(p.asnumpy(changed), want, rtol=5e-4, atol=5e-4)
+
+
+def test_padding_declines_float64_and_small(hip):
+    rng = np.random.default_rng(8303)
+    for rows, dtype in ((33, np.float64), (31, np.float32)):
+        left = rng.normal(size=(rows, 17)).astype(dtype)
+        right = rng.normal(size=(17, 65)).astype(dtype)
+        compiled = p.compile(lambda x, y: p.matmul(x, y), padding=True)
+        a, b = p.asarray(left, backend=hip), p.asarray(right, backend=hip)
+        assert not any(s["kind"] == "padded_matmul" for s in compiled.explain(a, b)["steps"])
+        np.testing.assert_allclose(p.asnumpy(compiled(a, b)), left @ right, rtol=5e-4, atol=5e-4)
+
+
+def test_padding_preserves_special_values_and_signed_zero(hip):
+    left = np.zeros((33, 17), np.float32)
+    right = np.zeros((17, 65), np.float32)
+    left[0, 0], right[0, 0] = np.nan, 1.0
+    left[1, 1], right[1, 1], right[1, 2] = np.inf, 0.0, 1.0
+    left[2, 2], right[2, 3] = -np.inf, 1.0
+    left[3, 3], right[3, 4] = -np.float32(0.0), 1.0
+    left[4, 4], right[4, 5] = np.float32(0.0), -1.0
+    left[5, 5], right[5, 6] = np.nextafter(np.float32(0), np.float32(1)), 1.0
+    left[6, 6], right[6, 7] = np.finfo(np.float32).tiny, 1.0
+    left[7, 7], right[7, 8] = np.finfo(np.float32).max, 1.0
+    a, b = p.asarray(left, backend=hip), p.asarray(right, backend=hip)
+    padded = p.asnumpy(p.matmul(a, b, padding=True))
+    ordinary = p.asnumpy(p.matmul(a, b))
+    for predicate in (np.isnan, np.isinf, np.isfinite):
+        np.testing.assert_array_equal(predicate(padded), predicate(ordinary))
+    for index in ((3, 4), (4, 5), (5, 6), (6, 7), (7, 8)):
+        assert np.signbit(padded[index]) == np.signbit(ordinary[index])
+        np.testing.assert_array_equal(padded[index], ordinary[index])
+    np.testing.assert_array_equal(p.asnumpy(a), left)

@@ -1,0 +1,100 @@
+"""GPU parity of GEMV/DOT (hp_gemv / hp_dot) against fp64 and exact oracles.
+
+Shapes and tolerances follow reference tests/test_cuda_gemv.py:133-222; the
+full-size case is BASELINE.json config 2 (16384^2 float32, x ~ N(0,1), seed 1)
+with the hip error bounded by 2x the error of the reference cooperative
+kernel's arithmetic order (oracle.kernels.gemv_lanes).
+"""
+
+import numpy as np
+import pytest
+
+import openpacho as p
+from oracle import exact, kernels
+
+pytestmark = pytest.mark.gpu
+
+SHAPES = [(33, 17), (129, 67), (33, 255), (33, 256), (33, 257), (513, 1023), (3, 4099), (2, 3, 257), (2, 1, 513), (7, 1024), (5, 2047)]
+
+
+@pytest.mark.parametrize("dtype", [np.float32, np.float64])
+@pytest.mark.parametrize("shape", SHAPES)
+def test_gemv_irregular_rows_batches_and_boundaries(hip, dtype, shape):
+    rng = np.random.default_rng(9101 + len(shape) + shape[-1])
+    left = rng.uniform(-1, 1, shape).astype(dtype)
+    right = rng.uniform(-1, 1, shape[-1]).astype(dtype)
+    actual = p.asarray(left, backend=hip) @ p.asarray(right, backend=hip)
+    expected = np.matmul(left.astype(np.float64), right.astype(np.float64))
+    tol = (5e-5, 5e-6) if dtype == np.float32 else (5e-12, 5e-13)
+    np.testing.assert_allclose(p.asnumpy(actual), expected, rtol=tol[0], atol=tol[1])
+
+
+def test_long_rows_cancellation_regression(hip):
+    rng = np.random.default_rng(941)
+    left = rng.uniform(-0.5, 0.5, (129, 8193)).astype(np.float32)
+    right = rng.uniform(-0.5, 0.5, 8193).astype(np.float32)
+    actual = p.asarray(left, backend=hip) @ p.asarray(right, backend=hip)
+    np.testing.assert_allclose(p.asnumpy(actual), left.astype(np.float64) @ right.astype(np.float64), rtol=5e-5, atol=5e-6)
+
+
+@pytest.mark.parametrize("length", [1, 63, 64, 65, 4096, 4097, 9001, 16384, 16385, 100003])
+@pytest.mark.parametrize("dtype", [np.float32, np.float64])
+def test_dot_tails_boundaries_and_long_partials(hip, length, dtype):
+    rng = np.random.default_rng(9102 + length)
+    left = rng.uniform(-1, 1, length).astype(dtype)
+    right = rng.uniform(-1, 1, length).astype(dtype)
+    actual = p.dot(p.asarray(left, backend=hip), p.asarray(right, backend=hip))
+    assert actual.shape == ()
+    want = float(exact.exact_dot(left, right))
+    tol = (5e-5, 5e-6) if dtype == np.float32 else (5e-12, 5e-13)
+    np.testing.assert_allclose(p.asnumpy(actual), want, rtol=tol[0], atol=tol[1])
+
+
+@pytest.mark.parametrize("dtype", [np.float32, np.float64])
+def test_gemv_cancellation_large_finite_signed_and_nonfinite(hip, dtype):
+    left = np.zeros((5, 257), dtype=dtype)
+    right = np.zeros(257, dtype=dtype)
+    left[0, :4] = [4096, -4096, 3, -3]
+    right[:4] = 1
+    left[1, 20], right[20] = 2.0**60, 2.0**-60
+    left[2, 10], right[10] = -0.0, 1.0
+    left[2, 11], right[11] = 0.0, 1.0
+    left[3, 60], right[60] = np.inf, 0.0
+    left[4, 61], right[61] = -np.inf, 1.0
+    values = p.asnumpy(p.asarray(left, backend=hip) @ p.asarray(right, backend=hip))
+    assert values[0] == 0 and values[1] == 1
+    assert values[2] == 0 and not np.signbit(values[2])
+    assert np.isnan(values[3]) and np.isneginf(values[4])
+
+
+def test_empty_and_zero_inner(hip):
+    for dtype in (np.float32, np.float64):
+        empty = p.asarray(np.zeros((0, 64), dtype), backend=hip) @ p.asarray(np.zeros(64, dtype), backend=hip)
+        assert empty.shape == (0,)
+        zero = p.asarray(np.zeros((3, 0), dtype), backend=hip) @ p.asarray(np.zeros(0, dtype), backend=hip)
+        np.testing.assert_array_equal(p.asnumpy(zero), np.zeros(3))
+        assert p.dot(p.asarray(np.zeros(0, dtype), backend=hip), p.asarray(np.zeros(0, dtype), backend=hip)).item() == 0
+
+
+def _rel_l2(value, reference):
+    return float(np.linalg.norm(value - reference) / np.linalg.norm(reference))
+
+
+def test_config2_gemv_16384_squared_within_2x_reference_kernel_error(hip):
+    n = 16384
+    rng = np.random.default_rng(1)
+    a = rng.uniform(-1, 1, (n, n)).astype(np.float32)
+    x = rng.standard_normal(n).astype(np.float32)
+    y = p.asnumpy(p.asarray(a, backend=hip) @ p.asarray(x, backend=hip))
+    assert y.shape == (n,) and np.isfinite(y).all()
+    oracle = np.empty(n)
+    for r in range(0, n, 2048):
+        oracle[r : r + 2048] = a[r : r + 2048].astype(np.float64) @ x.astype(np.float64)
+    hip_error = _rel_l2(y, oracle)
+    rows = np.arange(0, n, 64)  # 256 sampled rows for the reference-order restatement
+    ref = kernels.gemv_lanes(a[rows], x)
+    ref_error = _rel_l2(ref, oracle[rows])
+    assert _rel_l2(y[rows], oracle[rows]) <= 2 * ref_error
+    assert hip_error < 1e-6
+    dot = p.dot(p.asarray(x, backend=hip), p.asarray(x, backend=hip)).item()
+    assert dot == pytest.approx(float(exact.exact_dot(x, x)), rel=1e-6)

@@ -1,0 +1,158 @@
+"""GPU parity of the Philox generator (hp_philox / hp_philox_words) against the oracle.
+
+Integer stream and the random/uniform transforms: bit-exact. Normal and
+exponential: the reference's tolerance (3e-6 float32, 1e-13 float64;
+reference tests/test_random.py:75-80). Inputs mirror the reference tests
+(seeds 0 / 42 / 2^64-1, counters across the 2^32 carry and the end of the
+2^64 space) plus BASELINE.json config 5 (2^28 samples from seed 42).
+"""
+
+import ctypes
+from pathlib import Path
+
+import numpy as np
+import pytest
+
+import openpacho as p
+from oracle import philox
+from oracle import numpy_backend as nb
+
+pytestmark = pytest.mark.gpu
+
+GOLDEN = Path(__file__).parent / "golden" / "reference_rng.npz"
+PARAMS = {"random": {}, "uniform": {"low": -3, "high": 7}, "normal": {"loc": 2, "scale": 3}, "exponential": {"scale": 2}}
+ORACLE_ARGS = {"random": (0, 1), "uniform": (-3, 7), "normal": (2, 3), "exponential": (0, 2)}
+
+
+def _words(backend, count, seed, start):
+    out = backend.empty((count, 4), np.uint32)
+    backend._call("hp_philox_words", ctypes.c_void_p(out.ptr), count, seed, start)
+    host = np.empty((count, 4), np.uint32)
+    backend._call("hp_d2h", ctypes.c_void_p(host.ctypes.data), ctypes.c_void_p(out.ptr), host.nbytes)
+    return host
+
+
+@pytest.mark.parametrize("seed", [0, 42, 2**64 - 1])
+@pytest.mark.parametrize("start,count", [(0, 4097), (2**32 - 3, 1000), (2**32 - 300, 600), (2**64 - 7, 7)])
+def test_integer_stream_is_bit_exact(hip, seed, start, count):
+    np.testing.assert_array_equal(_words(hip, count, seed, start), philox.c_words(count, seed, start))
+
+
+@pytest.mark.parametrize("dtype", ["float32", "float64"])
+@pytest.mark.parametrize("start", [0, 2**32 - 3, 2**32 - 700, 2**64 - 1029])
+@pytest.mark.parametrize("count", [1, 3, 1029, 4096])
+def test_random_and_uniform_are_bit_exact(hip, dtype, start, count):
+    if start + count > 2**64:
+        pytest.skip("past the counter space")
+    for dist, kwargs in (("random", {}), ("uniform", {"low": -3, "high": 7})):
+        rng = p.random.default_rng(2**64 - 1, backend=hip)
+        rng._counter = start
+        got = p.asnumpy(getattr(rng, dist)(size=count, dtype=dtype, **kwargs))
+        want = philox.c_uniform(dtype, count, 2**64 - 1, start, dist, kwargs.get("low", 0), kwargs.get("high", 1))
+        np.testing.assert_array_equal(got, want, err_msg=f"{dist} {dtype} start={start}")
+
+
+@pytest.mark.parametrize("dtype", ["float32", "float64"])
+@pytest.mark.parametrize("dist", ["normal", "exponential"])
+def test_transcendental_transforms_within_reference_tolerance(hip, dtype, dist):
+    tol = 3e-6 if dtype == "float32" else 1e-13
+    for seed, start in ((2**64 - 1, 0), (42, 2**32 - 3)):
+        rng = p.random.default_rng(seed, backend=hip)
+        rng._counter = start
+        got = p.asnumpy(getattr(rng, dist)(size=(33, 17), dtype=dtype, **PARAMS[dist]))
+        first, second = ORACLE_ARGS[dist]
+        want = nb.random(dist, dtype, (33, 17), seed, start, first, second)
+        np.testing.assert_allclose(got, want, rtol=tol, atol=tol)
+
+
+def test_matches_reference_numpy_backend_golden_samples(hip):
+    with np.load(GOLDEN) as data:
+        golden = {k: data[k] for k in data.files}
+    for key, expected in golden.items():
+        dist, dtype, seed, start = key.split("|")
+        rng = p.random.default_rng(int(seed), backend=hip)
+        rng._counter = int(start)
+        got = p.asnumpy(getattr(rng, dist)(size=expected.shape[0], dtype=dtype, **PARAMS[dist]))
+        if dist in ("random", "uniform"):
+            np.testing.assert_array_equal(got, expected, err_msg=key)
+        else:
+            tol = 3e-6 if dtype == "float32" else 1e-13
+            np.testing.assert_allclose(got, expected, rtol=tol, atol=tol, err_msg=key)
+
+
+def test_split_calls_replay_the_same_stream(hip):
+    for dist, kwargs in PARAMS.items():
+        whole = p.asnumpy(getattr(p.random.default_rng(7, backend=hip), dist)(size=(33, 17), dtype="float32", **kwargs))
+        replay = p.random.default_rng(7, backend=hip)
+        parts = np.concatenate(
+            [p.asnumpy(getattr(replay, dist)(size=n, dtype="float32", **kwargs)) for n in (1, 127, 0, 433)]
+        )
+        np.testing.assert_array_equal(parts, whole.ravel())
+
+
+def test_carry_exhaustion_and_empty(hip):
+    rng = p.random.default_rng(0, backend=hip)
+    ref = p.random.default_rng(0, backend="numpy")
+    for start in (2**32 - 3, 2**64 - 7):
+        rng._counter = ref._counter = start
+        np.testing.assert_array_equal(p.asnumpy(rng.random(7, dtype="float32")), p.asnumpy(ref.random(7, dtype="float32")))
+    with pytest.raises(OverflowError):
+        rng.random(1, dtype="float32")
+    assert rng.random((0, 17), dtype="float32").shape == (0, 17)
+
+
+def test_ranges_scalars_and_no_host_upload(hip, monkeypatch):
+    def forbidden(*args, **kwargs):
+        raise AssertionError("RNG must not upload a host-generated matrix")
+
+    monkeypatch.setattr(hip, "upload", forbidden)
+    rng = p.random.default_rng(17, backend=hip)
+    assert rng.random(dtype="float32").shape == ()
+    for low, high in [(-3, 7), (1, np.nextafter(np.float32(1), np.float32(2))), (2, 2)]:
+        values = p.asnumpy(rng.uniform(low, high, (17, 33), dtype="float32"))
+        assert (values >= low).all()
+        assert (values < high).all() if high > low else (values == low).all()
+    np.testing.assert_array_equal(p.asnumpy(rng.normal(3, 0, 65, dtype="float32")), 3)
+    np.testing.assert_array_equal(p.asnumpy(rng.exponential(0, 65, dtype="float32")), 0)
+
+
+@pytest.mark.parametrize("distribution", ["random", "uniform", "normal", "exponential"])
+def test_statistical_smoke(hip, distribution):
+    values = p.asnumpy(getattr(p.random.default_rng(47, backend=hip), distribution)(size=(513, 513), dtype="float32"))
+    values = values.astype(float).ravel()
+    assert np.all(np.isfinite(values))
+    mean, variance = (0.5, 1 / 12) if distribution in ("random", "uniform") else ((0, 1) if distribution == "normal" else (1, 1))
+    assert abs(values.mean() - mean) < 0.015
+    assert abs(values.var() - variance) < 0.025
+    assert abs(np.corrcoef(values[:-1], values[1:])[0, 1]) < 0.015
+
+
+def test_config5_full_stream_2_28_random_is_bit_exact(hip):
+    """2^28 samples from seed 42, whole stream compared."""
+    n = 1 << 28
+    got = p.asnumpy(p.random.default_rng(42, backend=hip).random(n, dtype="float32"))
+    want = philox.c_uniform("float32", n, 42, 0)
+    assert np.array_equal(got, want)
+    # Chained calls continue the stream (counter n onwards).
+    rng = p.random.default_rng(42, backend=hip)
+    rng._counter = n
+    tail = p.asnumpy(rng.uniform(size=4096, dtype="float32"))
+    np.testing.assert_array_equal(tail, philox.c_uniform("float32", 4096, 42, n, "uniform", 0, 1))
+
+
+def test_config5_full_size_normal_and_exponential_properties(hip):
+    n = 1 << 28
+    rng = p.random.default_rng(42, backend=hip)
+    normal = rng.normal(0, 1, n, dtype="float32")
+    expo = rng.exponential(1, n, dtype="float32")
+    head = p.asnumpy(normal[:65536])
+    want = nb.random("normal", "float32", (65536,), 42, 0, 0, 1)
+    np.testing.assert_allclose(head, want, rtol=3e-6, atol=3e-6)
+    for values, mean, var in ((normal, 0.0, 1.0), (expo, 1.0, 1.0)):
+        total = float(p.sum(values.astype(np.float64)).item())
+        square = float(p.sum((values * values).astype(np.float64)).item())
+        m = total / n
+        assert abs(m - mean) < 1e-3 and abs(square / n - m * m - var) < 2e-3
+    tail = p.asnumpy(expo[n - 65536 :])
+    want = nb.random("exponential", "float32", (65536,), 42, 2 * n - 65536, 0, 1)
+    np.testing.assert_allclose(tail, want, rtol=3e-6, atol=3e-6)

@@ -1,0 +1,175 @@
+"""Pinning the restatements of the reference custom kernels and the exact oracles."""
+
+import math
+from fractions import Fraction
+from pathlib import Path
+
+import numpy as np
+import pytest
+
+from oracle import exact, kernels, padding
+from oracle import numpy_backend as nb
+
+GOLDEN_NORM = Path(__file__).parent / "golden" / "reference_norm.npz"
+
+
+# ---- exact oracles -----------------------------------------------------------------
+
+
+def test_exact_dot_closed_forms():
+    assert exact.exact_dot([1.0, 2.0, 3.0], [4.0, 5.0, 6.0]) == 32
+    # Catastrophic cancellation: float arithmetic returns 0, the exact value is 1.
+    a = np.array([2.0**60, 1.0, -(2.0**60)])
+    b = np.array([1.0, 1.0, 1.0])
+    assert float(np.dot(a, b)) == 0.0
+    assert exact.exact_dot(a, b) == 1
+    # Extreme binary exponents stay exact.
+    assert exact.exact_dot([2.0**-1074, 2.0**1000], [2.0**1000, 2.0**-1074]) == Fraction(2, 2**74)
+    x = np.float32(0.1)
+    assert exact.exact_dot([x], [x]) == Fraction(*float(x).as_integer_ratio()) ** 2
+
+
+def test_exact_norm_known_values_and_fsum_agreement():
+    assert exact.norm_exact([3.0, 4.0]) == 5.0
+    assert exact.norm_exact([5.0, 12.0]) == 13.0
+    assert exact.norm_exact([1e300, 1e300]) == pytest.approx(1e300 * math.sqrt(2), rel=1e-16)
+    assert exact.norm_exact([1e-300] * 4) == pytest.approx(2e-300, rel=1e-16)
+    rng = np.random.default_rng(5)
+    x = rng.uniform(-1, 1, 1000).astype(np.float32)
+    # float32 squares are exact in float64; fsum is correctly rounded.
+    fsum = math.sqrt(math.fsum(float(v) * float(v) for v in x))
+    assert exact.norm_exact(x) == pytest.approx(fsum, rel=2e-16)
+
+
+def test_extended_norm_matches_exact_on_extreme_inputs():
+    rng = np.random.default_rng(11)
+    x = 10.0 ** rng.uniform(-300, 300, 2000) * (rng.integers(0, 2, 2000) * 2 - 1)
+    assert float(exact.norm_extended(x)) == pytest.approx(exact.norm_exact(x), rel=1e-18)
+    rows = rng.uniform(-1, 1, (4, 300))
+    got = exact.norm_extended(rows, axis=1).reshape(-1)
+    for r in range(4):
+        assert float(got[r]) == pytest.approx(exact.norm_exact(rows[r]), rel=1e-18)
+
+
+# ---- reference custom-kernel restatements -----------------------------------------------
+
+
+def test_gemm_sequential_is_the_sequential_float32_loop():
+    rng = np.random.default_rng(1)
+    a = rng.uniform(-1, 1, (5, 37)).astype(np.float32)
+    b = rng.uniform(-1, 1, (37, 6)).astype(np.float32)
+    rows, cols = np.meshgrid(range(5), range(6), indexing="ij")
+    got = kernels.gemm_sequential(a, b, rows.ravel(), cols.ravel()).reshape(5, 6)
+    for i in range(5):
+        for j in range(6):
+            acc = np.float32(0)
+            for k in range(37):
+                acc = np.float32(acc + np.float32(a[i, k] * b[k, j]))
+            assert got[i, j] == acc
+    # Exactly representable terms: any order gives the exact integer result.
+    ints = np.arange(12, dtype=np.float32).reshape(3, 4)
+    assert kernels.gemm_sequential(ints, ints.T.copy(), [2], [1])[0] == float(ints[2] @ ints[1])
+
+
+def test_gemv_lanes_order_and_exact_cases():
+    x = np.arange(1, 301, dtype=np.float64)
+    assert kernels.gemv_lanes(x, np.ones(300)) == 300 * 301 / 2
+    a = np.zeros((5, 257), np.float32)
+    v = np.zeros(257, np.float32)
+    a[0, :4] = [4096, -4096, 3, -3]
+    v[:4] = 1
+    a[1, 20], v[20] = 2.0**60, 2.0**-60
+    got = kernels.gemv_lanes(a, v)
+    assert got[0] == 0 and got[1] == 1
+    # Brute force of the documented order on a small vector: lane sums then tree.
+    rng = np.random.default_rng(3)
+    y = rng.uniform(-1, 1, 300).astype(np.float32)
+    lanes = [np.float32(0)] * 128
+    for j in range(300):
+        lanes[j % 128] = np.float32(lanes[j % 128] + np.float32(y[j] * y[j]))
+    step = 64
+    while step:
+        for lane in range(step):
+            lanes[lane] = np.float32(lanes[lane] + lanes[lane + step])
+        step //= 2
+    assert kernels.gemv_lanes(y, y) == lanes[0]
+
+
+def test_long_dot_uses_1024_term_chunks_then_reduce():
+    rng = np.random.default_rng(9)
+    x = rng.uniform(-1, 1, 9001).astype(np.float32)
+    chunks = [kernels.gemv_lanes(x[i : i + 1024], x[i : i + 1024]) for i in range(0, 9001, 1024)]
+    assert kernels.gemv_lanes(x, x) == kernels.reduce_lanes(np.array(chunks, np.float32))
+    assert kernels.gemv_lanes(x, x) == pytest.approx(float(x.astype(np.float64) @ x), rel=1e-5)
+
+
+@pytest.mark.parametrize(
+    "values,expected",
+    [([0.0, 0.0], 0.0), ([np.inf, 1.0], np.inf), ([np.nan, np.inf], np.nan), ([-3.0, 4.0], 5.0)],
+)
+def test_pair_merge_special_values(values, expected):
+    got = kernels.norm_pair_merge(np.asarray(values, np.float64))
+    assert math.isnan(got) if math.isnan(expected) else got == expected
+
+
+@pytest.mark.parametrize("dtype,small,large", [(np.float32, 1e-25, 1e25), (np.float64, 1e-200, 1e200)])
+@pytest.mark.parametrize("length", [2, 4099, 8193])
+def test_pair_merge_extreme_constants_and_chunk_passes(dtype, small, large, length):
+    for scale in (small, large):
+        x = np.full(length, scale, dtype)
+        got = kernels.norm_pair_merge(x)
+        want = abs(float(dtype(scale))) * math.sqrt(length)
+        assert float(got) == pytest.approx(want, rel=2e-6)
+
+
+def test_pair_merge_error_against_exact_is_small():
+    rng = np.random.default_rng(2)
+    x = (10.0 ** rng.uniform(-30, 30, 5000) * (rng.integers(0, 2, 5000) * 2 - 1)).astype(np.float32)
+    ref = exact.norm_exact(x)
+    assert abs(float(kernels.norm_pair_merge(x)) - ref) / ref < 2e-6
+
+
+def test_reduce_lanes_matches_sum_for_exact_terms():
+    assert kernels.reduce_lanes(np.ones(10000, np.float32)) == 10000
+    assert kernels.reduce_lanes(np.arange(5000, dtype=np.float64)) == 5000 * 4999 / 2
+
+
+# ---- NumPy-backend norm against the reference's own outputs ------------------------------
+
+
+def test_numpy_backend_norm_reproduces_reference_golden():
+    with np.load(GOLDEN_NORM) as data:
+        golden = {k: data[k] for k in data.files}
+    for dtype in ("float32", "float64"):
+        x = golden[f"loguniform|{dtype}|input"]
+        np.testing.assert_allclose(nb.norm(x), golden[f"loguniform|{dtype}|norm"], rtol=1e-6 if dtype == "float32" else 1e-15)
+        cube = golden[f"cube|{dtype}|input"]
+        for axis in ((2, 0), 1, None):
+            key = "none" if axis is None else str(axis)
+            np.testing.assert_allclose(
+                nb.norm(cube, axis=axis, keepdims=True), golden[f"cube|{dtype}|axis={key}"], rtol=1e-6
+            )
+        rows = golden[f"rows|{dtype}|input"]
+        np.testing.assert_allclose(nb.norm(rows, axis=1), golden[f"rows|{dtype}|norm"], rtol=1e-6)
+        # The reference values themselves sit within float rounding of the exact norm.
+        ref = exact.norm_exact(x)
+        assert abs(float(golden[f"loguniform|{dtype}|norm"]) - ref) / ref < (2e-6 if dtype == "float32" else 1e-14)
+
+
+# ---- padding plan closed form ----------------------------------------------------------
+
+
+def test_padding_closed_form_matches_reference_worked_values():
+    p = padding.plan((33, 17), (17, 65))
+    assert p["padded_input_shapes"] == ((64, 32), (32, 96))
+    assert p["padded_output_shape"] == (64, 96)
+    assert p["scratch_bytes"] == 45056 and p["copy_dispatches"] == 3 and p["dispatch_count"] == 4
+    p = padding.plan((2, 1, 33, 17), (1, 3, 17, 65))
+    assert p["padded_input_shapes"] == ((2, 1, 64, 32), (1, 3, 32, 96))
+    assert p["padded_output_shape"] == (2, 3, 64, 96)
+    p = padding.plan((64, 32), (32, 96))
+    assert p["scratch_bytes"] == 0 and p["dispatch_count"] == 1
+    assert padding.plan((4097, 3001), (3001, 2049))["scratch_bytes"] == 109_039_616
+    for a, b in [((31, 16), (16, 32)), ((0, 32), (32, 96))]:
+        assert padding.plan(a, b) is None
+    assert padding.plan((33, 17), (17, 65), "float64") is None
