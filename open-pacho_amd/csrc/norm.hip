@@ -189,7 +189,9 @@ __global__ __launch_bounds__(1024) void norm_merge_kernel(const T* __restrict__ 
   }
 }
 
-// Strided reduction axis (inner > 1): one thread per output, two passes.
+// Strided reduction axis (inner > 1): one thread per output, two passes over
+// the column (max, then compensated scaled sum of squares); lanes read
+// adjacent columns, so every load instruction is coalesced.
 template <typename T>
 __global__ __launch_bounds__(kBlock) void norm_cols_kernel(const T* __restrict__ x, T* __restrict__ out,
                                                            int64_t outer, int64_t reduced, int64_t inner) {
@@ -203,13 +205,17 @@ __global__ __launch_bounds__(kBlock) void norm_cols_kernel(const T* __restrict__
     if (isnan(m) || isinf(m) || m == T(0)) {
       result = m;
     } else {
+      // Neumaier-compensated sum: one thread walks the whole strided column.
       const int e = dexponent(m);
-      T t = T(0);
+      T t = T(0), carry = T(0);
       for (int64_t r = 0; r < reduced; ++r) {
         const T s = dldexp(base[r * inner], -e);
-        t = t + s * s;
+        const T term = s * s;
+        const T next = t + term;
+        carry += (t >= term) ? (t - next) + term : (term - next) + t;
+        t = next;
       }
-      result = dldexp(dsqrt(t), e);
+      result = dldexp(dsqrt(t + carry), e);
     }
     out[g] = result;
   }

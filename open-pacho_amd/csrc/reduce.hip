@@ -10,6 +10,9 @@
 // fixed-order merge of the four wave results. Rows longer than kChunk leave
 // one partial per chunk and are reduced again. Strided axes use one thread
 // per output element.
+#include <limits>
+#include <type_traits>
+
 #include "common.h"
 
 namespace {
@@ -136,9 +139,21 @@ __global__ __launch_bounds__(kBlock) void reduce_cols_kernel(const T* __restrict
   for (int64_t g = int64_t(blockIdx.x) * blockDim.x + threadIdx.x; g < outer * inner; g += stride) {
     const int64_t o = g / inner, i = g - o * inner;
     const T* base = x + o * reduced * inner + i;
-    T acc = C::identity();
-    for (int64_t r = 0; r < reduced; ++r) acc = C::apply(acc, base[r * inner]);
-    out[g] = acc;
+    if constexpr (OP == HP_SUM && std::is_floating_point<T>::value) {
+      // Neumaier-compensated sum: one thread walks the whole strided column.
+      T acc = T(0), carry = T(0);
+      for (int64_t r = 0; r < reduced; ++r) {
+        const T v = base[r * inner];
+        const T next = acc + v;
+        carry += (fabs(acc) >= fabs(v)) ? (acc - next) + v : (v - next) + acc;
+        acc = next;
+      }
+      out[g] = acc + carry;
+    } else {
+      T acc = C::identity();
+      for (int64_t r = 0; r < reduced; ++r) acc = C::apply(acc, base[r * inner]);
+      out[g] = acc;
+    }
   }
 }
 
