@@ -18,6 +18,7 @@ namespace {
 
 constexpr int kBlock = 256;
 constexpr int kLoads = 16;  // 16-byte loads per lane per chunk
+constexpr int kResidentGroupsPerCU = 8;
 
 template <typename T>
 struct Traits;
@@ -57,14 +58,7 @@ __device__ __forceinline__ double dsqrt(double x) { return sqrt(x); }
 // max|.| that propagates NaN from either side.
 template <typename T>
 __device__ __forceinline__ T nan_max(T a, T b) {
-  return (isnan(a) || a > b) ? a : (isnan(b) ? b : b);
-}
-
-template <typename T>
-__device__ __forceinline__ T wave_nan_max(T v) {
-#pragma unroll
-  for (int o = 32; o > 0; o >>= 1) v = nan_max(v, __shfl_xor(v, o, 64));
-  return v;
+  return (isnan(a) || a > b) ? a : b;
 }
 
 // Pair algebra on (k, t): norm^2 = 4^k * t for finite k; k = -inf means 0.
@@ -102,79 +96,128 @@ __device__ __forceinline__ Pair<T> wave_merge(Pair<T> p) {
   return p;
 }
 
+__device__ __forceinline__ float dfma(float a, float b, float c) { return fmaf(a, b, c); }
+__device__ __forceinline__ double dfma(double a, double b, double c) { return fma(a, b, c); }
+__device__ __forceinline__ float dmax(float a, float b) { return fmaxf(a, b); }
+__device__ __forceinline__ double dmax(double a, double b) { return fmax(a, b); }
+
 // Reduce registers `v[0..n)` (zeros beyond the valid range) to a wave pair.
+// The max pass uses the NaN-dropping hardware max (one instruction per
+// element): a NaN then reaches the sum of squares and makes t NaN. Only when
+// the max is +inf or 0 (so no sum is formed) are the registers re-scanned for
+// NaN, which keeps NaN ahead of Inf.
 template <typename T, int N>
 __device__ __forceinline__ Pair<T> registers_to_pair(const T (&v)[N]) {
   T m = T(0);
 #pragma unroll
-  for (int i = 0; i < N; ++i) m = nan_max(dabs(v[i]), m);
-  m = wave_nan_max(m);
-  if (isnan(m)) return {T(NAN), T(0)};
-  if (isinf(m)) return {T(INFINITY), T(0)};
-  if (m == T(0)) return {T(-INFINITY), T(0)};
+  for (int i = 0; i < N; ++i) m = dmax(m, dabs(v[i]));
+#pragma unroll
+  for (int o = 32; o > 0; o >>= 1) m = dmax(m, __shfl_xor(m, o, 64));
+  if (isinf(m) || m == T(0)) {
+    bool nan = false;
+#pragma unroll
+    for (int i = 0; i < N; ++i) nan = nan || isnan(v[i]);
+    nan = __any(nan);
+    if (nan) return {T(NAN), T(0)};
+    return isinf(m) ? Pair<T>{T(INFINITY), T(0)} : Pair<T>{T(-INFINITY), T(0)};
+  }
   const int e = dexponent(m);
   T t = T(0);
 #pragma unroll
   for (int i = 0; i < N; ++i) {
     const T s = dldexp(v[i], -e);
-    t = t + s * s;
+    t = dfma(s, s, t);
   }
   t = hpd::wave_sum(t);
+  if (isnan(t)) return {T(NAN), T(0)};
   return {T(e), t};
 }
 
-// One wave per (row, chunk) of contiguous rows.
-template <typename T, bool kVector>
+// Contiguous rows, persistent: wave w of the grid handles units (row, chunk)
+// w, w + W, w + 2W, ... (W waves in the grid), so each round of the grid reads
+// one contiguous stretch of memory. Modes:
+//   kFinal   one chunk per row: write the row's norm;
+//   kPairs   several rows of several chunks: one pair per unit;
+//   kRunning a single row: every wave folds its chunks into a running pair
+//            and each workgroup writes one pair (few pairs left to merge).
+constexpr int kFinal = 0, kPairs = 1, kRunning = 2;
+
+template <typename T, bool kVector, int MODE>
 __global__ __launch_bounds__(kBlock) void norm_rows_kernel(const T* __restrict__ x, T* __restrict__ out,
-                                                           int64_t outer, int64_t reduced, int64_t chunks,
-                                                           bool final) {
+                                                           int64_t outer, int64_t reduced, int64_t chunks) {
   using V = typename Traits<T>::V;
   constexpr int W = Traits<T>::width;
   constexpr int N = kLoads * W;
-  const int lane = threadIdx.x & 63;
-  const int64_t g = int64_t(blockIdx.x) * (kBlock / 64) + (threadIdx.x >> 6);
-  if (g >= outer * chunks) return;
-  const int64_t o = g / chunks, ch = g - o * chunks;
-  const int64_t begin = ch * chunk_len<T>();
-  const int64_t len = reduced - begin < chunk_len<T>() ? reduced - begin : chunk_len<T>();
-  const T* base = x + o * reduced + begin;
-  T v[N];
-  if (kVector && len == chunk_len<T>()) {
-    const V* bv = reinterpret_cast<const V*>(base);
-    V q[kLoads];
+  const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
+  const int64_t units = outer * chunks;
+  const int64_t stride = int64_t(gridDim.x) * (kBlock / 64);
+  Pair<T> running = {T(-INFINITY), T(0)};
+  for (int64_t g = int64_t(blockIdx.x) * (kBlock / 64) + wave; g < units; g += stride) {
+    const int64_t o = g / chunks, ch = g - o * chunks;
+    const int64_t begin = ch * chunk_len<T>();
+    const int64_t len = reduced - begin < chunk_len<T>() ? reduced - begin : chunk_len<T>();
+    const T* base = x + o * reduced + begin;
+    T v[N];
+    if (kVector && len == chunk_len<T>()) {
+      const V* bv = reinterpret_cast<const V*>(base);
+      V q[kLoads];
 #pragma unroll
-    for (int i = 0; i < kLoads; ++i) q[i] = __builtin_nontemporal_load(bv + i * 64 + lane);
+      for (int i = 0; i < kLoads; ++i) q[i] = __builtin_nontemporal_load(bv + i * 64 + lane);
 #pragma unroll
-    for (int i = 0; i < kLoads; ++i)
+      for (int i = 0; i < kLoads; ++i)
 #pragma unroll
-      for (int w = 0; w < W; ++w) v[i * W + w] = q[i][w];
-  } else {
+        for (int w = 0; w < W; ++w) v[i * W + w] = q[i][w];
+    } else {
 #pragma unroll
-    for (int i = 0; i < N; ++i) {
-      const int64_t e = int64_t(i) * 64 + lane;
-      v[i] = e < len ? base[e] : T(0);
+      for (int i = 0; i < N; ++i) {
+        const int64_t e = int64_t(i) * 64 + lane;
+        v[i] = e < len ? base[e] : T(0);
+      }
+    }
+    const Pair<T> p = registers_to_pair<T, N>(v);
+    if (MODE == kRunning) {
+      running = merge(running, p);
+    } else if (lane == 0) {
+      if (MODE == kFinal) {
+        out[o] = finish(p);
+      } else {
+        out[2 * g] = p.k;
+        out[2 * g + 1] = p.t;
+      }
     }
   }
-  const Pair<T> p = registers_to_pair<T, N>(v);
-  if (lane == 0) {
-    if (final) {
-      out[o] = finish(p);
-    } else {
-      out[2 * g] = p.k;
-      out[2 * g + 1] = p.t;
+  if (MODE == kRunning) {
+    __shared__ T ks[kBlock / 64], ts[kBlock / 64];
+    if (lane == 0) {
+      ks[wave] = running.k;
+      ts[wave] = running.t;
+    }
+    __syncthreads();
+    if (threadIdx.x == 0) {
+      Pair<T> total = {ks[0], ts[0]};
+      for (int w = 1; w < kBlock / 64; ++w) total = merge(total, Pair<T>{ks[w], ts[w]});
+      out[2 * blockIdx.x] = total.k;
+      out[2 * blockIdx.x + 1] = total.t;
     }
   }
 }
 
-// One workgroup per row merges that row's chunk pairs in index order.
+// Pair merge pass: workgroup g merges pairs [c*kMerge, (c+1)*kMerge) of row
+// o = g / groups_out (c = g % groups_out) into one pair, or, in the last pass,
+// into the row's final norm. Passes repeat until one pair per row remains.
+constexpr int64_t kMerge = 4096;
+
 template <typename T>
-__global__ __launch_bounds__(1024) void norm_merge_kernel(const T* __restrict__ pairs, T* __restrict__ out,
-                                                          int64_t chunks) {
-  __shared__ T ks[16], ts[16];
-  const int64_t o = blockIdx.x;
+__global__ __launch_bounds__(kBlock) void norm_merge_kernel(const T* __restrict__ pairs, T* __restrict__ out,
+                                                            int64_t chunks, int64_t groups_out, bool final) {
+  __shared__ T ks[kBlock / 64], ts[kBlock / 64];
+  const int64_t g = blockIdx.x;
+  const int64_t o = g / groups_out, c = g - o * groups_out;
+  const int64_t begin = c * kMerge;
+  const int64_t end = begin + kMerge < chunks ? begin + kMerge : chunks;
   const T* row = pairs + 2 * o * chunks;
   Pair<T> p = {T(-INFINITY), T(0)};
-  for (int64_t c = threadIdx.x; c < chunks; c += blockDim.x) p = merge(p, Pair<T>{row[2 * c], row[2 * c + 1]});
+  for (int64_t i = begin + threadIdx.x; i < end; i += kBlock) p = merge(p, Pair<T>{row[2 * i], row[2 * i + 1]});
   p = wave_merge(p);
   const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
   if (lane == 0) {
@@ -184,8 +227,13 @@ __global__ __launch_bounds__(1024) void norm_merge_kernel(const T* __restrict__ 
   __syncthreads();
   if (threadIdx.x == 0) {
     Pair<T> total = {ks[0], ts[0]};
-    for (int w = 1; w < int(blockDim.x >> 6); ++w) total = merge(total, Pair<T>{ks[w], ts[w]});
-    out[o] = finish(total);
+    for (int w = 1; w < kBlock / 64; ++w) total = merge(total, Pair<T>{ks[w], ts[w]});
+    if (final) {
+      out[o] = finish(total);
+    } else {
+      out[2 * g] = total.k;
+      out[2 * g + 1] = total.t;
+    }
   }
 }
 
@@ -232,27 +280,45 @@ void run_norm(hp_ctx* ctx, const T* x, T* out, int64_t outer, int64_t reduced, i
     return;
   }
   const int64_t chunks = hp::ceil_div(reduced, chunk_len<T>());
-  const int64_t waves = outer * chunks;
-  const int64_t grid = hp::ceil_div(waves, kBlock / 64);
-  hp::require(grid <= hp::kMaxGrid, "norm input too large for one launch");
+  const int64_t units = outer * chunks;
   const bool vector = reinterpret_cast<uintptr_t>(x) % 16 == 0 && (reduced * int64_t(sizeof(T))) % 16 == 0;
-  T* target = out;
+  const int mode = chunks == 1 ? kFinal : (outer == 1 ? kRunning : kPairs);
+  // Enough resident waves to keep HBM busy; the grid loops over the rest.
+  const int64_t resident = int64_t(ctx->compute_units) * kResidentGroupsPerCU;
+  int64_t grid = hp::ceil_div(units, kBlock / 64);
+  if (grid > resident) grid = resident;
   T* pairs = nullptr;
-  if (chunks > 1) {
-    pairs = static_cast<T*>(hp::scratch_alloc(ctx, size_t(waves) * 2 * sizeof(T)));
+  T* target = out;
+  int64_t remaining = 1;
+  if (mode != kFinal) {
+    remaining = mode == kRunning ? grid : chunks;
+    pairs = static_cast<T*>(hp::scratch_alloc(ctx, size_t(mode == kRunning ? grid : units) * 2 * sizeof(T)));
     target = pairs;
   }
+#define PACHO_NORM_LAUNCH(VEC, MODE_)                                                                           \
+  norm_rows_kernel<T, VEC, MODE_><<<grid, kBlock, 0, ctx->stream>>>(x, target, outer, reduced, chunks)
   if (vector) {
-    norm_rows_kernel<T, true><<<grid, kBlock, 0, ctx->stream>>>(x, target, outer, reduced, chunks, chunks == 1);
+    if (mode == kFinal) PACHO_NORM_LAUNCH(true, kFinal);
+    else if (mode == kRunning) PACHO_NORM_LAUNCH(true, kRunning);
+    else PACHO_NORM_LAUNCH(true, kPairs);
   } else {
-    norm_rows_kernel<T, false><<<grid, kBlock, 0, ctx->stream>>>(x, target, outer, reduced, chunks, chunks == 1);
+    if (mode == kFinal) PACHO_NORM_LAUNCH(false, kFinal);
+    else if (mode == kRunning) PACHO_NORM_LAUNCH(false, kRunning);
+    else PACHO_NORM_LAUNCH(false, kPairs);
   }
+#undef PACHO_NORM_LAUNCH
   hp::check_launch("norm_rows");
-  if (chunks > 1) {
-    hp::require(outer <= hp::kMaxGrid, "too many rows for one launch");
-    norm_merge_kernel<T><<<outer, 1024, 0, ctx->stream>>>(pairs, out, chunks);
+  // Pair modes always finish with at least one merge pass (it writes `out`).
+  while (mode != kFinal && (pairs != out)) {
+    const int64_t groups = hp::ceil_div(remaining, kMerge);
+    const bool last = groups == 1;
+    T* next = last ? out : static_cast<T*>(hp::scratch_alloc(ctx, size_t(outer * groups) * 2 * sizeof(T)));
+    hp::require(outer * groups <= hp::kMaxGrid, "too many rows for one launch");
+    norm_merge_kernel<T><<<outer * groups, kBlock, 0, ctx->stream>>>(pairs, next, remaining, groups, last);
     hp::check_launch("norm_merge");
     hp::scratch_free(ctx, pairs);
+    pairs = next;
+    remaining = groups;
   }
 }
 
