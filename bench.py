@@ -263,6 +263,14 @@ def bench_extras(p, hip, only, skip_cpu):
         flops = 2.0 * 64 * 512 * 768 * 1024
         extra["gemm_f32_batched_64x512x1024x768"] = {"value": round(flops / (ms * 1e-3) / 1e9, 1), "unit": "GFLOP/s", "kernel_ms": round(ms, 4), "roofline": roofline("mfma", flops, ms)}
         del a, b
+    if only and "copy" in only:
+        # Calibration for rocprofv3 --pmc: a plain 1 GiB float32 copy
+        # (hipRTC elementwise cast kernel) moves exactly 2^30 B each way.
+        n = 1 << 28
+        src = p.random.default_rng(9, backend=hip).random(n, dtype="float32")
+        ms, wall = timer.run(lambda: src.copy(), 5)
+        extra["copy_f32_2^28"] = {"value": round(2 * n * 4 / (ms * 1e-3) / 1e9, 1), "unit": "GB/s", "kernel_us": round(ms * 1e3, 2)}
+        del src
     if want("mlp"):
         rng = p.random.default_rng(42, backend=hip)
         widths = (4096, 4096, 4096, 1024)
@@ -298,7 +306,7 @@ def main(argv=None):
     parser.add_argument("--steps", type=int, default=10)
     parser.add_argument("--warmup", type=int, default=3)
     parser.add_argument("--skip-cpu", action="store_true", help="omit the CPU baselines")
-    parser.add_argument("--only", default="", help="comma-separated extras to run (gemv,norm,rng,gemm_f64,gemm_padded,gemm_batched,mlp); 'none' for the headline only")
+    parser.add_argument("--only", default="", help="comma-separated extras to run (gemv,norm,rng,gemm_f64,gemm_padded,gemm_batched,mlp; copy = PMC calibration, only when named); 'none' for the headline only")
     args = parser.parse_args(argv)
     if args.gpus != 1:
         print(

@@ -40,8 +40,6 @@ _C_SCALARS = {
     np.dtype("float32"): ctypes.c_float,
     np.dtype("float64"): ctypes.c_double,
 }
-# Workgroup tile of the fp32 GEMM kernel (M, K, N).
-GEMM_TILE_F32 = (256, 16, 128)
 
 
 def hip_devices():
@@ -400,11 +398,32 @@ class HIPBackend:
         return dims, ra, rb
 
     def prepare_padded_matmul(self, ashape, bshape, shape, dtype):
-        from ._padding import prepare_register_padding
+        from ._hip_padding import prepare
 
-        return prepare_register_padding(
-            self, ashape, bshape, shape, dtype, _pad_copy, _padded_gemm, kernel_tile=GEMM_TILE_F32
-        )
+        return prepare(self, ashape, bshape, shape, dtype)
+
+    def pad_copy(self, array, shape):
+        """Pad (with +0 words) or crop ``array`` into a new buffer of ``shape``."""
+        shape = tuple(shape)
+        if len(shape) != array.ndim or shape[:-2] != array.shape[:-2]:
+            raise ValueError("padding copies keep the batch prefix and rank")
+        if array.dtype.itemsize not in (4, 8):
+            raise TypeError("padding copies move 4- or 8-byte words")
+        out = self.empty(shape, array.dtype)
+        if prod(shape):
+            with self._active():
+                self._call(
+                    "hp_pad_copy",
+                    array.dtype.itemsize,
+                    ctypes.c_void_p(array._data.ptr),
+                    ctypes.c_void_p(out.ptr),
+                    prod(shape[:-2]),
+                    array.shape[-2],
+                    array.shape[-1],
+                    shape[-2],
+                    shape[-1],
+                )
+        return out
 
     def norm(self, a, axes, keepdims, dtype):
         dtype = self.validate_dtype(dtype)
@@ -479,30 +498,3 @@ class HIPBackend:
             self.close()
         except Exception:  # noqa: BLE001 - interpreter shutdown only
             pass
-
-
-def _pad_copy(backend, array, shape):
-    """Pad (with +0 words) or crop ``array`` into a new buffer of ``shape``."""
-    shape = tuple(shape)
-    if len(shape) != array.ndim or shape[:-2] != array.shape[:-2]:
-        raise ValueError("padding copies keep the batch prefix and rank")
-    out = backend.empty(shape, array.dtype)
-    batch = prod(shape[:-2])
-    if prod(shape):
-        with backend._active():
-            backend._call(
-                "hp_pad_copy",
-                array.dtype.itemsize,
-                ctypes.c_void_p(array._data.ptr),
-                ctypes.c_void_p(out.ptr),
-                batch,
-                array.shape[-2],
-                array.shape[-1],
-                shape[-2],
-                shape[-1],
-            )
-    return out
-
-
-def _padded_gemm(backend, a, b, shape):
-    return backend.matmul(a, b, tuple(shape), a.dtype)

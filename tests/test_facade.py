@@ -13,7 +13,7 @@ import numpy as np
 import pytest
 
 import openpacho as p
-from openpacho._padding import prepare_register_padding
+from openpacho import _hip_padding
 from openpacho.backends import NumpyBackend
 from openpacho.exceptions import BackendMismatchError, BackendUnavailableError, UnsupportedDtypeError
 
@@ -292,7 +292,7 @@ class _NoAlloc:
 
 
 def _plan(ashape, bshape, shape, dtype=np.float32, **kw):
-    return prepare_register_padding(_NoAlloc(), ashape, bshape, shape, dtype, None, None, **kw)
+    return _hip_padding.prepare(_NoAlloc(), ashape, bshape, shape, dtype, **kw)
 
 
 def test_padding_metadata():
@@ -309,3 +309,5 @@ def test_padding_metadata():
     assert _plan((33, 17), (17, 65), (33, 65), max_buffer_bytes=24575) is None
     big = _plan((4097, 3001), (3001, 2049), (4097, 2049))
     assert big.explain()["scratch_bytes"] == 109_039_616
+    assert big.explain()["bounds_checks_removed"] is False
+    assert _plan((512, 64), (64, 256), (512, 256)).explain()["bounds_checks_removed"] is True
