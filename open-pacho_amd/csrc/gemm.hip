@@ -8,9 +8,9 @@
 // Data path per K slice: global -> registers (prefetch of slice s+1 while
 // slice s is multiplied) -> LDS (double-buffered, one barrier per slice) ->
 // 16-byte LDS reads -> MFMA. LDS holds both operands k-contiguous: A as
-// [m][k] (a plain copy of a row-major tile) and B as [n][k] (transposed in
-// registers on the way in). A lane of MFMA lane group g = lane/16 then reads
-// four consecutive k values with one ds_read_b128 and feeds them to four
+// [m][k] (a copy of a row-major tile) and B as [n][k] (each lane loads one
+// column's k values as scalars, so the transposition costs no shuffles). A
+// lane of MFMA lane group g = lane/16 then reads four consecutive k values with one ds_read_b128 and feeds them to four
 // MFMAs, i.e. MFMA number q contracts k = {q, 4+q, 8+q, 12+q}; A and B use
 // the same permutation, so every product of the slice is summed exactly once.
 //
@@ -19,8 +19,8 @@
 // rows, so the workgroups resident on one XCD share A and B panels in its L2.
 //
 // Modes: 0 = interior (no guards; M, N, K multiples of the tile and 16-byte
-// aligned rows), 1 = guarded vector loads (K % 4 == 0, N % 2 == 0 for fp32),
-// 2 = guarded scalar loads (any shape). Guarded loads fill zeros, so edge
+// aligned rows), 1 = guarded vector loads of A (K % 4 == 0 for fp32, K even
+// for fp64), 2 = guarded scalar loads (any shape). Guarded loads fill zeros, so edge
 // tiles contract against +0 padding, and stores are masked.
 //
 // Reference semantics: _gemm.py:24-137 (per-batch broadcast offsets
@@ -28,8 +28,6 @@
 #include "common.h"
 
 namespace {
-
-typedef float f32x2 __attribute__((ext_vector_type(2)));
 
 struct BatchDesc {
   int rank;
@@ -77,16 +75,22 @@ __device__ __forceinline__ void batch_offsets(int64_t batch, const BatchDesc& bd
 namespace f32 {
 
 constexpr int BM = 256, BN = 128, BK = 16;
-constexpr int SA = BK + 4;  // LDS row stride (floats) of the [m][k] and [n][k] tiles
-constexpr int SB = BK + 4;
+constexpr int S = BK;  // LDS row stride (floats): 16-float rows, swizzled quads
 constexpr int kThreads = 256;
+
+// LDS rows hold 4 quads of 4 consecutive k values; quad q of row r is stored
+// at slot q ^ ((r >> 1) & 3). Rows are 16 floats (64 B), so a ds_read_b128 by
+// lanes reading rows r0..r0+15 at one logical quad, a ds_write_b128 of 4 rows x
+// 4 quads, and the B writes of 16 consecutive n at one quad all land on
+// distinct banks (measured: removes the LDS bank conflicts of padded rows).
+__device__ __forceinline__ int swizzle(int row) { return (row >> 1) & 3; }
 
 template <int MODE>
 __global__ __launch_bounds__(kThreads, 2) void kernel(const float* __restrict__ A, const float* __restrict__ B,
                                                       float* __restrict__ C, int64_t M, int64_t N, int64_t K,
                                                       BatchDesc bd, TileMap tmap) {
-  __shared__ __attribute__((aligned(16))) float As[2][BM * SA];
-  __shared__ __attribute__((aligned(16))) float Bs[2][BN * SB];
+  __shared__ __attribute__((aligned(16))) float As[2][BM * S];
+  __shared__ __attribute__((aligned(16))) float Bs[2][BN * S];
 
   const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
   const int wm = wave >> 1, wn = wave & 1;
@@ -100,22 +104,28 @@ __global__ __launch_bounds__(kThreads, 2) void kernel(const float* __restrict__ 
   const int64_t m0 = ti * BM, n0 = tj * BN;
 
   // Global -> register assignment. A: 4 float4 per thread (rows tid/4 + 64i,
-  // k quad tid%4). B: rows k0 + 4*(tid/64) + s (s < 4), columns 2*(tid%64)+{0,1}.
-  int a_row[4];
-  const int a_k = (tid & 3) * 4;
+  // k quad tid%4). B: column n = tid%128, k quads 2*(tid/128) + {0, 1}
+  // (8 scalar loads; 64 lanes read 256 contiguous bytes of one B row).
+  int a_row[4], a_lds[4];
+  const int a_kq = tid & 3;
 #pragma unroll
-  for (int i = 0; i < 4; ++i) a_row[i] = (tid >> 2) + 64 * i;
-  const int b_k = (tid >> 6) * 4;
-  const int b_n = (tid & 63) * 2;
+  for (int i = 0; i < 4; ++i) {
+    a_row[i] = (tid >> 2) + 64 * i;
+    a_lds[i] = a_row[i] * S + 4 * (a_kq ^ swizzle(a_row[i]));
+  }
+  const int b_n = tid & (BN - 1);
+  const int b_q = (tid / BN) * 2;
+  const int b_lds0 = b_n * S + 4 * (b_q ^ swizzle(b_n));
+  const int b_lds1 = b_n * S + 4 * ((b_q + 1) ^ swizzle(b_n));
 
   hpd::f32x4 ra[4];
-  f32x2 rb[4];
+  float rb[2][4];
 
   auto load_slice = [&](int64_t k0) {
 #pragma unroll
     for (int i = 0; i < 4; ++i) {
       const int64_t row = m0 + a_row[i];
-      const int64_t kk = k0 + a_k;
+      const int64_t kk = k0 + 4 * a_kq;
       const float* p = Ab + row * K + kk;
       if (MODE == 0) {
         ra[i] = *reinterpret_cast<const hpd::f32x4*>(p);
@@ -127,31 +137,26 @@ __global__ __launch_bounds__(kThreads, 2) void kernel(const float* __restrict__ 
         for (int e = 0; e < 4; ++e) ra[i][e] = (row < M && kk + e < K) ? p[e] : 0.f;
       }
     }
+    const int64_t col = n0 + b_n;
 #pragma unroll
-    for (int s = 0; s < 4; ++s) {
-      const int64_t kr = k0 + b_k + s;
-      const int64_t col = n0 + b_n;
-      const float* p = Bb + kr * N + col;
-      if (MODE == 0) {
-        rb[s] = *reinterpret_cast<const f32x2*>(p);
-      } else if (MODE == 1) {
-        const bool ok = kr < K && col < N;
-        rb[s] = ok ? *reinterpret_cast<const f32x2*>(p) : f32x2{0.f, 0.f};
-      } else {
-        rb[s][0] = (kr < K && col < N) ? p[0] : 0.f;
-        rb[s][1] = (kr < K && col + 1 < N) ? p[1] : 0.f;
+    for (int q = 0; q < 2; ++q) {
+#pragma unroll
+      for (int e = 0; e < 4; ++e) {
+        const int64_t kr = k0 + 4 * (b_q + q) + e;
+        if (MODE == 0) {
+          rb[q][e] = Bb[kr * N + col];
+        } else {
+          rb[q][e] = (kr < K && col < N) ? Bb[kr * N + col] : 0.f;
+        }
       }
     }
   };
 
   auto store_slice = [&](int buf) {
 #pragma unroll
-    for (int i = 0; i < 4; ++i) *reinterpret_cast<hpd::f32x4*>(&As[buf][a_row[i] * SA + a_k]) = ra[i];
-#pragma unroll
-    for (int nn = 0; nn < 2; ++nn) {
-      const hpd::f32x4 v = {rb[0][nn], rb[1][nn], rb[2][nn], rb[3][nn]};
-      *reinterpret_cast<hpd::f32x4*>(&Bs[buf][(b_n + nn) * SB + b_k]) = v;
-    }
+    for (int i = 0; i < 4; ++i) *reinterpret_cast<hpd::f32x4*>(&As[buf][a_lds[i]]) = ra[i];
+    *reinterpret_cast<hpd::f32x4*>(&Bs[buf][b_lds0]) = hpd::f32x4{rb[0][0], rb[0][1], rb[0][2], rb[0][3]};
+    *reinterpret_cast<hpd::f32x4*>(&Bs[buf][b_lds1]) = hpd::f32x4{rb[1][0], rb[1][1], rb[1][2], rb[1][3]};
   };
 
   hpd::f32x4 acc[8][4];
@@ -160,8 +165,10 @@ __global__ __launch_bounds__(kThreads, 2) void kernel(const float* __restrict__ 
 #pragma unroll
     for (int j = 0; j < 4; ++j) acc[i][j] = hpd::f32x4{0.f, 0.f, 0.f, 0.f};
 
-  const int a_read = (wm * 128 + (lane & 15)) * SA + (lane >> 4) * 4;
-  const int b_read = (wn * 64 + (lane & 15)) * SB + (lane >> 4) * 4;
+  // Rows read by a lane differ by multiples of 16, so the swizzle of every
+  // row it reads equals that of (lane & 15).
+  const int a_read = (wm * 128 + (lane & 15)) * S + 4 * ((lane >> 4) ^ swizzle(lane & 15));
+  const int b_read = (wn * 64 + (lane & 15)) * S + 4 * ((lane >> 4) ^ swizzle(lane & 15));
   const int64_t slices = (K + BK - 1) / BK;
 
   load_slice(0);
@@ -172,9 +179,9 @@ __global__ __launch_bounds__(kThreads, 2) void kernel(const float* __restrict__ 
     if (s + 1 < slices) load_slice((s + 1) * BK);
     hpd::f32x4 a[8], b[4];
 #pragma unroll
-    for (int i = 0; i < 8; ++i) a[i] = *reinterpret_cast<const hpd::f32x4*>(&As[cur][a_read + 16 * i * SA]);
+    for (int i = 0; i < 8; ++i) a[i] = *reinterpret_cast<const hpd::f32x4*>(&As[cur][a_read + 16 * i * S]);
 #pragma unroll
-    for (int j = 0; j < 4; ++j) b[j] = *reinterpret_cast<const hpd::f32x4*>(&Bs[cur][b_read + 16 * j * SB]);
+    for (int j = 0; j < 4; ++j) b[j] = *reinterpret_cast<const hpd::f32x4*>(&Bs[cur][b_read + 16 * j * S]);
 #pragma unroll
     for (int q = 0; q < 4; ++q)
 #pragma unroll
@@ -351,9 +358,9 @@ void prepare(int64_t m, int64_t n, int64_t batch, int64_t bm, int64_t bn, TileMa
   hp::require(tm.total <= hp::kMaxGrid, "GEMM has too many tiles for one launch");
 }
 
-bool strides_aligned(const BatchDesc& bd, int64_t elems_per_16b) {
+bool a_strides_aligned(const BatchDesc& bd, int64_t elems_per_16b) {
   for (int d = 0; d < bd.rank; ++d) {
-    if (bd.a_stride[d] % elems_per_16b || bd.b_stride[d] % elems_per_16b) return false;
+    if (bd.a_stride[d] % elems_per_16b) return false;
   }
   return true;
 }
@@ -363,7 +370,7 @@ void run_f32(hp_ctx* ctx, const float* a, const float* b, float* c, int64_t m, i
   using namespace f32;
   TileMap tm;
   prepare(m, n, batch, BM, BN, tm);
-  const bool vec_ok = aligned16(a) && aligned16(b) && k % 4 == 0 && n % 4 == 0 && strides_aligned(bd, 4);
+  const bool vec_ok = aligned16(a) && k % 4 == 0 && a_strides_aligned(bd, 4);
   const bool interior = vec_ok && m % BM == 0 && n % BN == 0 && k % BK == 0;
   if (interior) {
     kernel<0><<<tm.total, kThreads, 0, ctx->stream>>>(a, b, c, m, n, k, bd, tm);
@@ -380,7 +387,7 @@ void run_f64(hp_ctx* ctx, const double* a, const double* b, double* c, int64_t m
   using namespace f64;
   TileMap tm;
   prepare(m, n, batch, BM, BN, tm);
-  const bool vec_ok = aligned16(a) && aligned16(b) && k % 2 == 0 && strides_aligned(bd, 2);
+  const bool vec_ok = aligned16(a) && k % 2 == 0 && a_strides_aligned(bd, 2);
   const bool interior = vec_ok && m % BM == 0 && n % BN == 0 && k % BK == 0;
   if (interior) {
     kernel<0><<<tm.total, kThreads, 0, ctx->stream>>>(a, b, c, m, n, k, bd, tm);
