@@ -10,21 +10,32 @@
 // 16-byte LDS reads -> MFMA. LDS holds both operands k-contiguous: A as
 // [m][k] (a copy of a row-major tile) and B as [n][k] (each lane loads one
 // column's k values as scalars, so the transposition costs no shuffles). A
-// lane of MFMA lane group g = lane/16 then reads four consecutive k values with one ds_read_b128 and feeds them to four
-// MFMAs, i.e. MFMA number q contracts k = {q, 4+q, 8+q, 12+q}; A and B use
-// the same permutation, so every product of the slice is summed exactly once.
+// lane of MFMA lane group g = lane/16 then reads four consecutive k values
+// with one ds_read_b128 and feeds them to four MFMAs, i.e. MFMA number q
+// contracts k = {q, 4+q, 8+q, 12+q}; A and B use the same permutation, so
+// every product of the slice is summed exactly once.
 //
-// Tile order: workgroup ids are renumbered so each XCD (ids i % 8) owns a
-// contiguous range of tiles, and tiles are visited in groups of kGroupM tile
-// rows, so the workgroups resident on one XCD share A and B panels in its L2.
+// Schedule. Tiles are numbered batch-major and, inside a batch, in groups of
+// kGroupM tile rows, so neighbouring tiles share A and B panels. Whole rounds
+// of resident workgroups (compute units x workgroups per CU) each take one
+// tile and its full K range; workgroup ids are renumbered so each XCD (ids
+// i % 8) owns a contiguous range of tiles and its L2 sees shared panels. The
+// tiles of a last, partly filled round are instead cut into equal runs of K
+// slices over every resident slot (stream-K): a worker's run covers the end
+// of one tile and the start of the next, and every cut piece goes to a
+// workspace. A second kernel adds the pieces of each cut tile in K order, so
+// results are deterministic. Without this, e.g. 289 tiles on 512 slots leave
+// most compute units with one tile while 33 run two in sequence.
 //
 // Modes: 0 = interior (no guards; M, N, K multiples of the tile and 16-byte
 // aligned rows), 1 = guarded vector loads of A (K % 4 == 0 for fp32, K even
-// for fp64), 2 = guarded scalar loads (any shape). Guarded loads fill zeros, so edge
-// tiles contract against +0 padding, and stores are masked.
+// for fp64), 2 = guarded scalar loads (any shape). Guarded loads fill zeros,
+// so edge tiles contract against +0 padding, and stores are masked.
 //
 // Reference semantics: _gemm.py:24-137 (per-batch broadcast offsets
 // _offset :13-21, never reads C), _cuda.py:493-518 and :619-636.
+#include <algorithm>
+
 #include "common.h"
 
 namespace {
@@ -40,12 +51,23 @@ struct TileMap {
   int64_t tiles_m, tiles_n, tiles_per_batch, total;
 };
 
-constexpr int64_t kGroupM = 8;
+// Division of the tile space between whole-tile workgroups and stream-K
+// workers. Logical tiles [0, dp_tiles) run whole; the K slices of tiles
+// [dp_tiles, total) are dealt out in consecutive runs, worker w owning
+// base + (w < extra) slices starting at sk_begin(w).
+struct Split {
+  int64_t dp_tiles;
+  int64_t workers;
+  int64_t base, extra;
+  int64_t slices;  // K slices per tile
+  void* partial;   // [workers][2][tile elements]: a worker's first and last cut piece
+};
 
-__device__ __forceinline__ void map_tile(int64_t bid, const TileMap& tm, int64_t& batch, int64_t& ti, int64_t& tj) {
-  int64_t t = bid;
-  const int64_t full = (tm.total / 8) * 8;
-  if (bid < full) t = (bid % 8) * (full / 8) + bid / 8;
+constexpr int64_t kGroupM = 8;
+constexpr int64_t kMinSlices = 8;  // shortest stream-K run
+
+__device__ __forceinline__ void logical_tile(int64_t t, const TileMap& tm, int64_t& batch, int64_t& ti,
+                                             int64_t& tj) {
   batch = t / tm.tiles_per_batch;
   t -= batch * tm.tiles_per_batch;
   const int64_t group = t / (kGroupM * tm.tiles_n);
@@ -54,6 +76,37 @@ __device__ __forceinline__ void map_tile(int64_t bid, const TileMap& tm, int64_t
   const int64_t r = t - group * kGroupM * tm.tiles_n;
   ti = first + r % gm;
   tj = r / gm;
+}
+
+// Consecutive ids of a count-long range, renumbered so that ids landing on one
+// XCD (ids i % 8) get a contiguous block of the range.
+__device__ __forceinline__ int64_t xcd_major(int64_t id, int64_t count) {
+  const int64_t full = (count / 8) * 8;
+  return id < full ? (id % 8) * (full / 8) + id / 8 : id;
+}
+
+__host__ __device__ __forceinline__ int64_t sk_begin(const Split& sp, int64_t w) {
+  return w * sp.base + (w < sp.extra ? w : sp.extra);
+}
+
+__device__ __forceinline__ int64_t sk_worker(const Split& sp, int64_t g) {
+  const int64_t long_runs = sp.extra * (sp.base + 1);
+  return g < long_runs ? g / (sp.base + 1) : sp.extra + (g - long_runs) / sp.base;
+}
+
+// First K slice of this workgroup's work and the end of it, both in the
+// concatenated slice space of its tile range; worker = -1 for whole tiles.
+__device__ __forceinline__ void work_range(const Split& sp, int64_t& g, int64_t& g_end, int64_t& worker) {
+  const int64_t bid = blockIdx.x;
+  if (bid < sp.dp_tiles) {
+    g = xcd_major(bid, sp.dp_tiles) * sp.slices;
+    g_end = g + sp.slices;
+    worker = -1;
+  } else {
+    worker = xcd_major(bid - sp.dp_tiles, sp.workers);
+    g = sp.dp_tiles * sp.slices + sk_begin(sp, worker);
+    g_end = sp.dp_tiles * sp.slices + sk_begin(sp, worker + 1);
+  }
 }
 
 __device__ __forceinline__ void batch_offsets(int64_t batch, const BatchDesc& bd, int64_t& a_off, int64_t& b_off) {
@@ -77,6 +130,8 @@ namespace f32 {
 constexpr int BM = 256, BN = 128, BK = 16;
 constexpr int S = BK;  // LDS row stride (floats): 16-float rows, swizzled quads
 constexpr int kThreads = 256;
+constexpr int FM = 8, FN = 4;  // MFMA blocks per wave
+constexpr int WM = 128, WN = 64;
 
 // LDS rows hold 4 quads of 4 consecutive k values; quad q of row r is stored
 // at slot q ^ ((r >> 1) & 3). Rows are 16 floats (64 B), so a ds_read_b128 by
@@ -85,23 +140,24 @@ constexpr int kThreads = 256;
 // distinct banks (measured: removes the LDS bank conflicts of padded rows).
 __device__ __forceinline__ int swizzle(int row) { return (row >> 1) & 3; }
 
+// Accumulator layout: lane holds column lane%16, rows 4*(lane/16) + r.
+struct Layout {
+  static constexpr int kBM = BM, kBN = BN, kFM = FM, kFN = FN;
+  static __device__ __forceinline__ int row(int wave, int i, int lane, int r) {
+    return (wave >> 1) * WM + 16 * i + 4 * (lane >> 4) + r;
+  }
+  static __device__ __forceinline__ int col(int wave, int j, int lane) { return (wave & 1) * WN + 16 * j + (lane & 15); }
+};
+
 template <int MODE>
 __global__ __launch_bounds__(kThreads, 2) void kernel(const float* __restrict__ A, const float* __restrict__ B,
                                                       float* __restrict__ C, int64_t M, int64_t N, int64_t K,
-                                                      BatchDesc bd, TileMap tmap) {
+                                                      BatchDesc bd, TileMap tmap, Split sp) {
   __shared__ __attribute__((aligned(16))) float As[2][BM * S];
   __shared__ __attribute__((aligned(16))) float Bs[2][BN * S];
 
   const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
   const int wm = wave >> 1, wn = wave & 1;
-  int64_t batch, ti, tj;
-  map_tile(blockIdx.x, tmap, batch, ti, tj);
-  int64_t a_off, b_off;
-  batch_offsets(batch, bd, a_off, b_off);
-  const float* Ab = A + a_off;
-  const float* Bb = B + b_off;
-  float* Cb = C + batch * M * N;
-  const int64_t m0 = ti * BM, n0 = tj * BN;
 
   // Global -> register assignment. A: 4 float4 per thread (rows tid/4 + 64i,
   // k quad tid%4). B: column n = tid%128, k quads 2*(tid/128) + {0, 1}
@@ -117,95 +173,128 @@ __global__ __launch_bounds__(kThreads, 2) void kernel(const float* __restrict__ 
   const int b_q = (tid / BN) * 2;
   const int b_lds0 = b_n * S + 4 * (b_q ^ swizzle(b_n));
   const int b_lds1 = b_n * S + 4 * ((b_q + 1) ^ swizzle(b_n));
-
-  hpd::f32x4 ra[4];
-  float rb[2][4];
-
-  auto load_slice = [&](int64_t k0) {
-#pragma unroll
-    for (int i = 0; i < 4; ++i) {
-      const int64_t row = m0 + a_row[i];
-      const int64_t kk = k0 + 4 * a_kq;
-      const float* p = Ab + row * K + kk;
-      if (MODE == 0) {
-        ra[i] = *reinterpret_cast<const hpd::f32x4*>(p);
-      } else if (MODE == 1) {
-        const bool ok = row < M && kk < K;
-        ra[i] = ok ? *reinterpret_cast<const hpd::f32x4*>(p) : hpd::f32x4{0.f, 0.f, 0.f, 0.f};
-      } else {
-#pragma unroll
-        for (int e = 0; e < 4; ++e) ra[i][e] = (row < M && kk + e < K) ? p[e] : 0.f;
-      }
-    }
-    const int64_t col = n0 + b_n;
-#pragma unroll
-    for (int q = 0; q < 2; ++q) {
-#pragma unroll
-      for (int e = 0; e < 4; ++e) {
-        const int64_t kr = k0 + 4 * (b_q + q) + e;
-        if (MODE == 0) {
-          rb[q][e] = Bb[kr * N + col];
-        } else {
-          rb[q][e] = (kr < K && col < N) ? Bb[kr * N + col] : 0.f;
-        }
-      }
-    }
-  };
-
-  auto store_slice = [&](int buf) {
-#pragma unroll
-    for (int i = 0; i < 4; ++i) *reinterpret_cast<hpd::f32x4*>(&As[buf][a_lds[i]]) = ra[i];
-    *reinterpret_cast<hpd::f32x4*>(&Bs[buf][b_lds0]) = hpd::f32x4{rb[0][0], rb[0][1], rb[0][2], rb[0][3]};
-    *reinterpret_cast<hpd::f32x4*>(&Bs[buf][b_lds1]) = hpd::f32x4{rb[1][0], rb[1][1], rb[1][2], rb[1][3]};
-  };
-
-  hpd::f32x4 acc[8][4];
-#pragma unroll
-  for (int i = 0; i < 8; ++i)
-#pragma unroll
-    for (int j = 0; j < 4; ++j) acc[i][j] = hpd::f32x4{0.f, 0.f, 0.f, 0.f};
-
   // Rows read by a lane differ by multiples of 16, so the swizzle of every
   // row it reads equals that of (lane & 15).
-  const int a_read = (wm * 128 + (lane & 15)) * S + 4 * ((lane >> 4) ^ swizzle(lane & 15));
-  const int b_read = (wn * 64 + (lane & 15)) * S + 4 * ((lane >> 4) ^ swizzle(lane & 15));
-  const int64_t slices = (K + BK - 1) / BK;
+  const int a_read = (wm * WM + (lane & 15)) * S + 4 * ((lane >> 4) ^ swizzle(lane & 15));
+  const int b_read = (wn * WN + (lane & 15)) * S + 4 * ((lane >> 4) ^ swizzle(lane & 15));
 
-  load_slice(0);
-  store_slice(0);
-  __syncthreads();
-  for (int64_t s = 0; s < slices; ++s) {
-    const int cur = int(s & 1);
-    if (s + 1 < slices) load_slice((s + 1) * BK);
-    hpd::f32x4 a[8], b[4];
-#pragma unroll
-    for (int i = 0; i < 8; ++i) a[i] = *reinterpret_cast<const hpd::f32x4*>(&As[cur][a_read + 16 * i * S]);
-#pragma unroll
-    for (int j = 0; j < 4; ++j) b[j] = *reinterpret_cast<const hpd::f32x4*>(&Bs[cur][b_read + 16 * j * S]);
-#pragma unroll
-    for (int q = 0; q < 4; ++q)
-#pragma unroll
-      for (int i = 0; i < 8; ++i)
-#pragma unroll
-        for (int j = 0; j < 4; ++j)
-          acc[i][j] = __builtin_amdgcn_mfma_f32_16x16x4f32(a[i][q], b[j][q], acc[i][j], 0, 0, 0);
-    if (s + 1 < slices) store_slice(cur ^ 1);
-    __syncthreads();
-  }
+  int64_t run_begin, run_end, worker;
+  work_range(sp, run_begin, run_end, worker);
+  // One piece of K slices [g, g_end) inside one tile. Straight-line calls
+  // rather than a loop over pieces keep the register allocation of a single
+  // tile (a loop back-edge costs ~90 spilled registers).
+  auto piece = [&](int64_t g, int64_t g_end, bool first_piece) {
+    const int64_t tile = g / sp.slices;
+    const int64_t s0 = g - tile * sp.slices;
+    const int64_t s1 = s0 + (g_end - g);
+    int64_t batch, ti, tj;
+    logical_tile(tile, tmap, batch, ti, tj);
+    int64_t a_off, b_off;
+    batch_offsets(batch, bd, a_off, b_off);
+    const float* Ab = A + a_off;
+    const float* Bb = B + b_off;
+    const int64_t m0 = ti * BM, n0 = tj * BN;
 
-  // Accumulator layout: lane holds column lane%16, rows 4*(lane/16) + r.
+    hpd::f32x4 ra[4];
+    float rb[2][4];
+
+    auto load_slice = [&](int64_t k0) {
 #pragma unroll
-  for (int i = 0; i < 8; ++i) {
+      for (int i = 0; i < 4; ++i) {
+        const int64_t row = m0 + a_row[i];
+        const int64_t kk = k0 + 4 * a_kq;
+        const float* p = Ab + row * K + kk;
+        if (MODE == 0) {
+          ra[i] = *reinterpret_cast<const hpd::f32x4*>(p);
+        } else if (MODE == 1) {
+          const bool ok = row < M && kk < K;
+          ra[i] = ok ? *reinterpret_cast<const hpd::f32x4*>(p) : hpd::f32x4{0.f, 0.f, 0.f, 0.f};
+        } else {
 #pragma unroll
-    for (int j = 0; j < 4; ++j) {
-      const int64_t col = n0 + wn * 64 + 16 * j + (lane & 15);
-#pragma unroll
-      for (int r = 0; r < 4; ++r) {
-        const int64_t row = m0 + wm * 128 + 16 * i + 4 * (lane >> 4) + r;
-        if (MODE == 0 || (row < M && col < N)) Cb[row * N + col] = acc[i][j][r];
+          for (int e = 0; e < 4; ++e) ra[i][e] = (row < M && kk + e < K) ? p[e] : 0.f;
+        }
       }
+      const int64_t col = n0 + b_n;
+#pragma unroll
+      for (int q = 0; q < 2; ++q) {
+#pragma unroll
+        for (int e = 0; e < 4; ++e) {
+          const int64_t kr = k0 + 4 * (b_q + q) + e;
+          if (MODE == 0) {
+            rb[q][e] = Bb[kr * N + col];
+          } else {
+            rb[q][e] = (kr < K && col < N) ? Bb[kr * N + col] : 0.f;
+          }
+        }
+      }
+    };
+
+    auto store_slice = [&](int buf) {
+#pragma unroll
+      for (int i = 0; i < 4; ++i) *reinterpret_cast<hpd::f32x4*>(&As[buf][a_lds[i]]) = ra[i];
+      *reinterpret_cast<hpd::f32x4*>(&Bs[buf][b_lds0]) = hpd::f32x4{rb[0][0], rb[0][1], rb[0][2], rb[0][3]};
+      *reinterpret_cast<hpd::f32x4*>(&Bs[buf][b_lds1]) = hpd::f32x4{rb[1][0], rb[1][1], rb[1][2], rb[1][3]};
+    };
+
+    hpd::f32x4 acc[FM][FN];
+#pragma unroll
+    for (int i = 0; i < FM; ++i)
+#pragma unroll
+      for (int j = 0; j < FN; ++j) acc[i][j] = hpd::f32x4{0.f, 0.f, 0.f, 0.f};
+
+    load_slice(s0 * BK);
+    store_slice(0);
+    __syncthreads();
+    for (int64_t s = s0; s < s1; ++s) {
+      const int cur = int((s - s0) & 1);
+      if (s + 1 < s1) load_slice((s + 1) * BK);
+      hpd::f32x4 a[FM], b[FN];
+#pragma unroll
+      for (int i = 0; i < FM; ++i) a[i] = *reinterpret_cast<const hpd::f32x4*>(&As[cur][a_read + 16 * i * S]);
+#pragma unroll
+      for (int j = 0; j < FN; ++j) b[j] = *reinterpret_cast<const hpd::f32x4*>(&Bs[cur][b_read + 16 * j * S]);
+#pragma unroll
+      for (int q = 0; q < 4; ++q)
+#pragma unroll
+        for (int i = 0; i < FM; ++i)
+#pragma unroll
+          for (int j = 0; j < FN; ++j)
+            acc[i][j] = __builtin_amdgcn_mfma_f32_16x16x4f32(a[i][q], b[j][q], acc[i][j], 0, 0, 0);
+      if (s + 1 < s1) store_slice(cur ^ 1);
+      // Also orders this piece's last LDS reads before the next piece's
+      // first LDS writes.
+      __syncthreads();
     }
-  }
+
+    if (s0 == 0 && s1 == sp.slices) {
+      float* Cb = C + batch * M * N;
+#pragma unroll
+      for (int i = 0; i < FM; ++i) {
+#pragma unroll
+        for (int j = 0; j < FN; ++j) {
+          const int64_t col = n0 + Layout::col(wave, j, lane);
+#pragma unroll
+          for (int r = 0; r < 4; ++r) {
+            const int64_t row = m0 + Layout::row(wave, i, lane, r);
+            if (MODE == 0 || (row < M && col < N)) Cb[row * N + col] = acc[i][j][r];
+          }
+        }
+      }
+    } else {
+      // Cut piece: whole accumulator tile to the worker's workspace slot, in
+      // register order (16 contiguous bytes per lane).
+      hpd::f32x4* slot = static_cast<hpd::f32x4*>(sp.partial) + (worker * 2 + (first_piece ? 0 : 1)) * (BM * BN / 4);
+#pragma unroll
+      for (int i = 0; i < FM; ++i)
+#pragma unroll
+        for (int j = 0; j < FN; ++j) slot[((wave * FM + i) * FN + j) * 64 + lane] = acc[i][j];
+    }
+  };
+  // A run is at most one tile long, so it covers the end of one tile and the
+  // start of the next at most.
+  const int64_t tile_end = (run_begin / sp.slices + 1) * sp.slices;
+  piece(run_begin, run_end < tile_end ? run_end : tile_end, true);
+  if (run_end > tile_end) piece(tile_end, run_end, false);
 }
 
 }  // namespace f32
@@ -218,26 +307,29 @@ constexpr int BM = 128, BN = 128, BK = 16;
 constexpr int SA = BK + 2;  // LDS row stride in doubles
 constexpr int SB = BK + 2;
 constexpr int kThreads = 256;
+constexpr int FM = 4, FN = 4;
+constexpr int WM = 64, WN = 64;
 
 typedef double f64x4 __attribute__((ext_vector_type(4)));
+
+// f64 accumulator layout: lane holds column lane%16, rows 4*r + lane/16.
+struct Layout {
+  static constexpr int kBM = BM, kBN = BN, kFM = FM, kFN = FN;
+  static __device__ __forceinline__ int row(int wave, int i, int lane, int r) {
+    return (wave >> 1) * WM + 16 * i + 4 * r + (lane >> 4);
+  }
+  static __device__ __forceinline__ int col(int wave, int j, int lane) { return (wave & 1) * WN + 16 * j + (lane & 15); }
+};
 
 template <int MODE>
 __global__ __launch_bounds__(kThreads, 2) void kernel(const double* __restrict__ A, const double* __restrict__ B,
                                                       double* __restrict__ C, int64_t M, int64_t N, int64_t K,
-                                                      BatchDesc bd, TileMap tmap) {
+                                                      BatchDesc bd, TileMap tmap, Split sp) {
   __shared__ __attribute__((aligned(16))) double As[2][BM * SA];
   __shared__ __attribute__((aligned(16))) double Bs[2][BN * SB];
 
   const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
   const int wm = wave >> 1, wn = wave & 1;
-  int64_t batch, ti, tj;
-  map_tile(blockIdx.x, tmap, batch, ti, tj);
-  int64_t a_off, b_off;
-  batch_offsets(batch, bd, a_off, b_off);
-  const double* Ab = A + a_off;
-  const double* Bb = B + b_off;
-  double* Cb = C + batch * M * N;
-  const int64_t m0 = ti * BM, n0 = tj * BN;
 
   // A: 4 double2 per thread (rows tid/8 + 32i, k pair tid%8).
   // B: column n = tid%128, k rows 8*(tid/128) + {0..7} (8 scalar loads).
@@ -247,103 +339,172 @@ __global__ __launch_bounds__(kThreads, 2) void kernel(const double* __restrict__
   for (int i = 0; i < 4; ++i) a_row[i] = (tid >> 3) + 32 * i;
   const int b_n = tid & 127;
   const int b_k = (tid >> 7) * 8;
-
-  hpd::f64x2 ra[4];
-  double rb[8];
-
-  auto load_slice = [&](int64_t k0) {
-#pragma unroll
-    for (int i = 0; i < 4; ++i) {
-      const int64_t row = m0 + a_row[i];
-      const int64_t kk = k0 + a_k;
-      const double* p = Ab + row * K + kk;
-      if (MODE == 0) {
-        ra[i] = *reinterpret_cast<const hpd::f64x2*>(p);
-      } else if (MODE == 1) {
-        const bool ok = row < M && kk < K;
-        ra[i] = ok ? *reinterpret_cast<const hpd::f64x2*>(p) : hpd::f64x2{0.0, 0.0};
-      } else {
-        ra[i][0] = (row < M && kk < K) ? p[0] : 0.0;
-        ra[i][1] = (row < M && kk + 1 < K) ? p[1] : 0.0;
-      }
-    }
-    const int64_t col = n0 + b_n;
-#pragma unroll
-    for (int s = 0; s < 8; ++s) {
-      const int64_t kr = k0 + b_k + s;
-      if (MODE == 0) {
-        rb[s] = Bb[kr * N + col];
-      } else {
-        rb[s] = (kr < K && col < N) ? Bb[kr * N + col] : 0.0;
-      }
-    }
-  };
-
-  auto store_slice = [&](int buf) {
-#pragma unroll
-    for (int i = 0; i < 4; ++i) *reinterpret_cast<hpd::f64x2*>(&As[buf][a_row[i] * SA + a_k]) = ra[i];
-#pragma unroll
-    for (int s = 0; s < 4; ++s) {
-      const hpd::f64x2 v = {rb[2 * s], rb[2 * s + 1]};
-      *reinterpret_cast<hpd::f64x2*>(&Bs[buf][b_n * SB + b_k + 2 * s]) = v;
-    }
-  };
-
-  f64x4 acc[4][4];
-#pragma unroll
-  for (int i = 0; i < 4; ++i)
-#pragma unroll
-    for (int j = 0; j < 4; ++j) acc[i][j] = f64x4{0.0, 0.0, 0.0, 0.0};
-
   // Lane group g = lane/16 reads k = 2g, 2g+1 (first half of the slice) and
   // 8 + 2g, 8 + 2g + 1 (second half): MFMA q in {0,1} per half.
-  const int a_read = (wm * 64 + (lane & 15)) * SA + (lane >> 4) * 2;
-  const int b_read = (wn * 64 + (lane & 15)) * SB + (lane >> 4) * 2;
-  const int64_t slices = (K + BK - 1) / BK;
+  const int a_read = (wm * WM + (lane & 15)) * SA + (lane >> 4) * 2;
+  const int b_read = (wn * WN + (lane & 15)) * SB + (lane >> 4) * 2;
 
-  load_slice(0);
-  store_slice(0);
-  __syncthreads();
-  for (int64_t s = 0; s < slices; ++s) {
-    const int cur = int(s & 1);
-    if (s + 1 < slices) load_slice((s + 1) * BK);
-#pragma unroll
-    for (int half = 0; half < 2; ++half) {
-      hpd::f64x2 a[4], b[4];
-#pragma unroll
-      for (int i = 0; i < 4; ++i)
-        a[i] = *reinterpret_cast<const hpd::f64x2*>(&As[cur][a_read + 16 * i * SA + 8 * half]);
-#pragma unroll
-      for (int j = 0; j < 4; ++j)
-        b[j] = *reinterpret_cast<const hpd::f64x2*>(&Bs[cur][b_read + 16 * j * SB + 8 * half]);
-#pragma unroll
-      for (int q = 0; q < 2; ++q)
-#pragma unroll
-        for (int i = 0; i < 4; ++i)
-#pragma unroll
-          for (int j = 0; j < 4; ++j)
-            acc[i][j] = __builtin_amdgcn_mfma_f64_16x16x4f64(a[i][q], b[j][q], acc[i][j], 0, 0, 0);
-    }
-    if (s + 1 < slices) store_slice(cur ^ 1);
-    __syncthreads();
-  }
+  int64_t run_begin, run_end, worker;
+  work_range(sp, run_begin, run_end, worker);
+  // One piece of K slices [g, g_end) inside one tile. Straight-line calls
+  // rather than a loop over pieces keep the register allocation of a single
+  // tile (a loop back-edge costs ~90 spilled registers).
+  auto piece = [&](int64_t g, int64_t g_end, bool first_piece) {
+    const int64_t tile = g / sp.slices;
+    const int64_t s0 = g - tile * sp.slices;
+    const int64_t s1 = s0 + (g_end - g);
+    int64_t batch, ti, tj;
+    logical_tile(tile, tmap, batch, ti, tj);
+    int64_t a_off, b_off;
+    batch_offsets(batch, bd, a_off, b_off);
+    const double* Ab = A + a_off;
+    const double* Bb = B + b_off;
+    const int64_t m0 = ti * BM, n0 = tj * BN;
 
-  // f64 accumulator layout: lane holds column lane%16, rows 4*r + lane/16.
+    hpd::f64x2 ra[4];
+    double rb[8];
+
+    auto load_slice = [&](int64_t k0) {
 #pragma unroll
-  for (int i = 0; i < 4; ++i) {
-#pragma unroll
-    for (int j = 0; j < 4; ++j) {
-      const int64_t col = n0 + wn * 64 + 16 * j + (lane & 15);
-#pragma unroll
-      for (int r = 0; r < 4; ++r) {
-        const int64_t row = m0 + wm * 64 + 16 * i + 4 * r + (lane >> 4);
-        if (MODE == 0 || (row < M && col < N)) Cb[row * N + col] = acc[i][j][r];
+      for (int i = 0; i < 4; ++i) {
+        const int64_t row = m0 + a_row[i];
+        const int64_t kk = k0 + a_k;
+        const double* p = Ab + row * K + kk;
+        if (MODE == 0) {
+          ra[i] = *reinterpret_cast<const hpd::f64x2*>(p);
+        } else if (MODE == 1) {
+          const bool ok = row < M && kk < K;
+          ra[i] = ok ? *reinterpret_cast<const hpd::f64x2*>(p) : hpd::f64x2{0.0, 0.0};
+        } else {
+          ra[i][0] = (row < M && kk < K) ? p[0] : 0.0;
+          ra[i][1] = (row < M && kk + 1 < K) ? p[1] : 0.0;
+        }
       }
+      const int64_t col = n0 + b_n;
+#pragma unroll
+      for (int s = 0; s < 8; ++s) {
+        const int64_t kr = k0 + b_k + s;
+        if (MODE == 0) {
+          rb[s] = Bb[kr * N + col];
+        } else {
+          rb[s] = (kr < K && col < N) ? Bb[kr * N + col] : 0.0;
+        }
+      }
+    };
+
+    auto store_slice = [&](int buf) {
+#pragma unroll
+      for (int i = 0; i < 4; ++i) *reinterpret_cast<hpd::f64x2*>(&As[buf][a_row[i] * SA + a_k]) = ra[i];
+#pragma unroll
+      for (int s = 0; s < 4; ++s) {
+        const hpd::f64x2 v = {rb[2 * s], rb[2 * s + 1]};
+        *reinterpret_cast<hpd::f64x2*>(&Bs[buf][b_n * SB + b_k + 2 * s]) = v;
+      }
+    };
+
+    f64x4 acc[FM][FN];
+#pragma unroll
+    for (int i = 0; i < FM; ++i)
+#pragma unroll
+      for (int j = 0; j < FN; ++j) acc[i][j] = f64x4{0.0, 0.0, 0.0, 0.0};
+
+    load_slice(s0 * BK);
+    store_slice(0);
+    __syncthreads();
+    for (int64_t s = s0; s < s1; ++s) {
+      const int cur = int((s - s0) & 1);
+      if (s + 1 < s1) load_slice((s + 1) * BK);
+#pragma unroll
+      for (int half = 0; half < 2; ++half) {
+        hpd::f64x2 a[FM], b[FN];
+#pragma unroll
+        for (int i = 0; i < FM; ++i)
+          a[i] = *reinterpret_cast<const hpd::f64x2*>(&As[cur][a_read + 16 * i * SA + 8 * half]);
+#pragma unroll
+        for (int j = 0; j < FN; ++j)
+          b[j] = *reinterpret_cast<const hpd::f64x2*>(&Bs[cur][b_read + 16 * j * SB + 8 * half]);
+#pragma unroll
+        for (int q = 0; q < 2; ++q)
+#pragma unroll
+          for (int i = 0; i < FM; ++i)
+#pragma unroll
+            for (int j = 0; j < FN; ++j)
+              acc[i][j] = __builtin_amdgcn_mfma_f64_16x16x4f64(a[i][q], b[j][q], acc[i][j], 0, 0, 0);
+      }
+      if (s + 1 < s1) store_slice(cur ^ 1);
+      __syncthreads();
     }
-  }
+
+    if (s0 == 0 && s1 == sp.slices) {
+      double* Cb = C + batch * M * N;
+#pragma unroll
+      for (int i = 0; i < FM; ++i) {
+#pragma unroll
+        for (int j = 0; j < FN; ++j) {
+          const int64_t col = n0 + Layout::col(wave, j, lane);
+#pragma unroll
+          for (int r = 0; r < 4; ++r) {
+            const int64_t row = m0 + Layout::row(wave, i, lane, r);
+            if (MODE == 0 || (row < M && col < N)) Cb[row * N + col] = acc[i][j][r];
+          }
+        }
+      }
+    } else {
+      f64x4* slot = static_cast<f64x4*>(sp.partial) + (worker * 2 + (first_piece ? 0 : 1)) * (BM * BN / 4);
+#pragma unroll
+      for (int i = 0; i < FM; ++i)
+#pragma unroll
+        for (int j = 0; j < FN; ++j) slot[((wave * FM + i) * FN + j) * 64 + lane] = acc[i][j];
+    }
+  };
+  // A run is at most one tile long, so it covers the end of one tile and the
+  // start of the next at most.
+  const int64_t tile_end = (run_begin / sp.slices + 1) * sp.slices;
+  piece(run_begin, run_end < tile_end ? run_end : tile_end, true);
+  if (run_end > tile_end) piece(tile_end, run_end, false);
 }
 
 }  // namespace f64
+
+// Adds the cut pieces of each stream-K tile in K order (workers in increasing
+// order own increasing K ranges) and stores the tile. Tiles that one worker
+// covered whole were stored by it. One thread per accumulator 4-vector.
+template <typename T, typename V, typename L>
+__global__ __launch_bounds__(256) void fixup_kernel(T* __restrict__ C, int64_t M, int64_t N, TileMap tmap,
+                                                    Split sp) {
+  constexpr int BM = L::kBM, BN = L::kBN, FM = L::kFM, FN = L::kFN;
+  constexpr int kVectors = BM * BN / 4;
+  constexpr int kBlocksPerTile = kVectors / 256;
+  const int64_t tl = blockIdx.x / kBlocksPerTile;
+  const int v = (blockIdx.x % kBlocksPerTile) * 256 + threadIdx.x;
+  const int64_t g0 = tl * sp.slices;
+  const int64_t w0 = sk_worker(sp, g0), w1 = sk_worker(sp, g0 + sp.slices - 1);
+  if (w0 == w1) return;
+  const V* partial = static_cast<const V*>(sp.partial);
+  // w0 holds the tile's K start: as its first piece when its run starts
+  // there, else as its last. Later workers start inside the tile.
+  V sum = partial[(w0 * 2 + (sk_begin(sp, w0) == g0 ? 0 : 1)) * kVectors + v];
+  for (int64_t w = w0 + 1; w <= w1; ++w) sum = sum + partial[w * 2 * kVectors + v];
+  const int lane = v & 63;
+  const int block = v >> 6;
+  const int wave = block / (FM * FN);
+  const int i = (block / FN) % FM;
+  const int j = block % FN;
+  int64_t batch, ti, tj;
+  logical_tile(sp.dp_tiles + tl, tmap, batch, ti, tj);
+  T* Cb = C + batch * M * N;
+  const int64_t col = tj * BN + L::col(wave, j, lane);
+#pragma unroll
+  for (int r = 0; r < 4; ++r) {
+    const int64_t row = ti * BM + L::row(wave, i, lane, r);
+    if (row < M && col < N) Cb[row * N + col] = sum[r];
+  }
+}
+
+template <typename T>
+__global__ __launch_bounds__(256) void zero_kernel(T* __restrict__ out, int64_t count) {
+  for (int64_t i = int64_t(blockIdx.x) * 256 + threadIdx.x; i < count; i += int64_t(gridDim.x) * 256) out[i] = T(0);
+}
 
 template <typename T>
 bool aligned16(const T* p) {
@@ -365,6 +526,55 @@ bool a_strides_aligned(const BatchDesc& bd, int64_t elems_per_16b) {
   return true;
 }
 
+template <typename F>
+int resident_per_cu(F kernel, int threads) {
+  int blocks = 0;
+  HP_CHECK(hipOccupancyMaxActiveBlocksPerMultiprocessor(&blocks, kernel, threads, 0));
+  hp::require(blocks > 0, "GEMM kernel does not fit on a compute unit");
+  return blocks;
+}
+
+// Whole tiles for every complete round of `slots` resident workgroups; the
+// tiles of an incomplete last round go to stream-K unless that round is
+// nearly full or K is too short to cut.
+Split plan_split(int64_t total, int64_t slices, int64_t slots) {
+  Split sp{};
+  sp.dp_tiles = total;
+  sp.slices = slices;
+  const int64_t rem = total % slots;
+  if (rem == 0 || 8 * rem >= 7 * slots || slices < 2 * kMinSlices) return sp;
+  sp.dp_tiles = total - rem;
+  const int64_t work = rem * slices;
+  sp.workers = std::min<int64_t>(slots, std::max<int64_t>(1, work / kMinSlices));
+  sp.base = work / sp.workers;
+  sp.extra = work % sp.workers;
+  // The kernels handle runs of at most one tile (two pieces): rem < slots
+  // gives base < slices when workers == slots, and base < 2 * kMinSlices <=
+  // slices otherwise.
+  if (sp.base + (sp.extra > 0 ? 1 : 0) > slices) hp::fail(HP_E_HIP, "internal: stream-K run longer than a tile");
+  return sp;
+}
+
+// Launches kernel (grid = whole tiles + stream-K workers) and, if tiles were
+// cut, the fixup over a pooled workspace.
+template <typename T, int BM, int BN, typename Main, typename Fix>
+void launch_split(hp_ctx* ctx, Main main, Fix fixup, int per_cu, int threads, const T* a, const T* b, T* c,
+                  int64_t m, int64_t n, int64_t k, const BatchDesc& bd, const TileMap& tm, int64_t bk,
+                  const char* name) {
+  Split sp = plan_split(tm.total, hp::ceil_div(k, bk), int64_t(ctx->compute_units) * per_cu);
+  if (sp.workers > 0) {
+    sp.partial = hp::scratch_alloc(ctx, size_t(sp.workers) * 2 * BM * BN * sizeof(T));
+  }
+  main<<<sp.dp_tiles + sp.workers, threads, 0, ctx->stream>>>(a, b, c, m, n, k, bd, tm, sp);
+  hp::check_launch(name);
+  if (sp.workers > 0) {
+    const int64_t cut = tm.total - sp.dp_tiles;
+    fixup<<<cut * (BM * BN / 4 / 256), 256, 0, ctx->stream>>>(c, m, n, tm, sp);
+    hp::check_launch(name);
+    hp::scratch_free(ctx, sp.partial);
+  }
+}
+
 void run_f32(hp_ctx* ctx, const float* a, const float* b, float* c, int64_t m, int64_t n, int64_t k,
              const BatchDesc& bd, int64_t batch) {
   using namespace f32;
@@ -372,14 +582,17 @@ void run_f32(hp_ctx* ctx, const float* a, const float* b, float* c, int64_t m, i
   prepare(m, n, batch, BM, BN, tm);
   const bool vec_ok = aligned16(a) && k % 4 == 0 && a_strides_aligned(bd, 4);
   const bool interior = vec_ok && m % BM == 0 && n % BN == 0 && k % BK == 0;
+  auto fix = fixup_kernel<float, hpd::f32x4, Layout>;
+  static const int occ0 = resident_per_cu(kernel<0>, kThreads);
+  static const int occ1 = resident_per_cu(kernel<1>, kThreads);
+  static const int occ2 = resident_per_cu(kernel<2>, kThreads);
   if (interior) {
-    kernel<0><<<tm.total, kThreads, 0, ctx->stream>>>(a, b, c, m, n, k, bd, tm);
+    launch_split<float, BM, BN>(ctx, kernel<0>, fix, occ0, kThreads, a, b, c, m, n, k, bd, tm, BK, "gemm_f32");
   } else if (vec_ok) {
-    kernel<1><<<tm.total, kThreads, 0, ctx->stream>>>(a, b, c, m, n, k, bd, tm);
+    launch_split<float, BM, BN>(ctx, kernel<1>, fix, occ1, kThreads, a, b, c, m, n, k, bd, tm, BK, "gemm_f32");
   } else {
-    kernel<2><<<tm.total, kThreads, 0, ctx->stream>>>(a, b, c, m, n, k, bd, tm);
+    launch_split<float, BM, BN>(ctx, kernel<2>, fix, occ2, kThreads, a, b, c, m, n, k, bd, tm, BK, "gemm_f32");
   }
-  hp::check_launch("gemm_f32");
 }
 
 void run_f64(hp_ctx* ctx, const double* a, const double* b, double* c, int64_t m, int64_t n, int64_t k,
@@ -389,14 +602,17 @@ void run_f64(hp_ctx* ctx, const double* a, const double* b, double* c, int64_t m
   prepare(m, n, batch, BM, BN, tm);
   const bool vec_ok = aligned16(a) && k % 2 == 0 && a_strides_aligned(bd, 2);
   const bool interior = vec_ok && m % BM == 0 && n % BN == 0 && k % BK == 0;
+  auto fix = fixup_kernel<double, f64x4, Layout>;
+  static const int occ0 = resident_per_cu(kernel<0>, kThreads);
+  static const int occ1 = resident_per_cu(kernel<1>, kThreads);
+  static const int occ2 = resident_per_cu(kernel<2>, kThreads);
   if (interior) {
-    kernel<0><<<tm.total, kThreads, 0, ctx->stream>>>(a, b, c, m, n, k, bd, tm);
+    launch_split<double, BM, BN>(ctx, kernel<0>, fix, occ0, kThreads, a, b, c, m, n, k, bd, tm, BK, "gemm_f64");
   } else if (vec_ok) {
-    kernel<1><<<tm.total, kThreads, 0, ctx->stream>>>(a, b, c, m, n, k, bd, tm);
+    launch_split<double, BM, BN>(ctx, kernel<1>, fix, occ1, kThreads, a, b, c, m, n, k, bd, tm, BK, "gemm_f64");
   } else {
-    kernel<2><<<tm.total, kThreads, 0, ctx->stream>>>(a, b, c, m, n, k, bd, tm);
+    launch_split<double, BM, BN>(ctx, kernel<2>, fix, occ2, kThreads, a, b, c, m, n, k, bd, tm, BK, "gemm_f64");
   }
-  hp::check_launch("gemm_f64");
 }
 
 }  // namespace
@@ -428,7 +644,13 @@ int hp_gemm(hp_ctx* ctx, int dtype, const void* a, const void* b, void* c, int64
     if (outputs == 0) return;
     require(c != nullptr, "null output");
     if (k == 0) {
-      HP_CHECK(hipMemsetAsync(c, 0, size_t(outputs) * hp::dtype_size(dtype), ctx->stream));
+      const int64_t grid = std::min<int64_t>(hp::ceil_div(outputs, 256), 65536);
+      if (dtype == HP_F32) {
+        zero_kernel<float><<<grid, 256, 0, ctx->stream>>>(static_cast<float*>(c), outputs);
+      } else {
+        zero_kernel<double><<<grid, 256, 0, ctx->stream>>>(static_cast<double*>(c), outputs);
+      }
+      hp::check_launch("gemm_zero");
       return;
     }
     require(a != nullptr && b != nullptr, "null input");

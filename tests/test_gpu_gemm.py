@@ -127,6 +127,37 @@ def test_kernel_modes_against_float64(hip, dtype, m, n, k):
     assert np.all(np.abs(got - want) <= bound * scale + 1e-30)
 
 
+# Tile counts that leave the last round of resident workgroups (256 compute
+# units x 2) partly filled, so their K slices are cut into stream-K runs and
+# summed by the fixup kernel: runs that cross tile boundaries (extra > 0),
+# single-tile problems cut over many workers, batched tiles, every load mode.
+STREAM_K_CASES = [
+    (np.float32, (), 512, 256, 1552),  # interior, 4 tiles x 97 slices, runs of 9 and 8
+    (np.float32, (), 31, 33, 4099),  # one tile cut over 32 workers
+    (np.float32, (), 1000, 700, 2000),  # guarded vector loads, 24 tiles
+    (np.float32, (), 777, 555, 1111),  # scalar loads (K odd)
+    (np.float32, (3,), 300, 200, 700),  # batched: 12 tiles
+    (np.float64, (), 1000, 1000, 2000),  # 64 tiles over 512 workers, extra > 0
+    (np.float64, (2,), 256, 384, 1024),  # interior fp64, batched
+    (np.float64, (), 129, 65, 3001),  # scalar loads fp64
+]
+
+
+@pytest.mark.parametrize("dtype,batch,m,n,k", STREAM_K_CASES)
+def test_stream_k_splits_against_float64_and_deterministic(hip, dtype, batch, m, n, k):
+    rng = np.random.default_rng(m + 3 * n + 7 * k)
+    a = rng.uniform(-1, 1, batch + (m, k)).astype(dtype)
+    b = rng.uniform(-1, 1, (k, n)).astype(dtype)
+    A, B = p.asarray(a, backend=hip), p.asarray(b, backend=hip)
+    got = p.asnumpy(A @ B)
+    again = p.asnumpy(A @ B)
+    np.testing.assert_array_equal(got, again)  # fixed K order: bitwise repeatable
+    want = a.astype(np.float64) @ b.astype(np.float64)
+    scale = np.abs(a).astype(np.float64) @ np.abs(b).astype(np.float64)
+    bound = (4e-7 if dtype == np.float32 else 8e-16) * np.sqrt(k) * 4
+    assert np.all(np.abs(got - want) <= bound * scale + 1e-30)
+
+
 def _sampled_error_ratio(a, b, got, samples, seed):
     """(hip error, reference-order error) over sampled outputs, exact oracle."""
     rng = np.random.default_rng(seed)
