@@ -1,19 +1,21 @@
 // MFMA GEMM for gfx950: C[b] = A[b'] @ B[b''] in fp32 and fp64.
 //
 // fp32: v_mfma_f32_16x16x4_f32 (measured 155 TFLOP/s peak on MI355X, against
-// 137 for the 32x32x2 form). Workgroup tile 256x128x16, four waves in a 2x2
-// grid, each wave 128x64 (8x4 MFMA blocks, 128 accumulators per lane).
+// 137 for the 32x32x2 form). Workgroup tile 256x256x16, eight waves in a 2x4
+// grid, each wave 128x64 (8x4 MFMA blocks, 128 accumulators per lane); one
+// workgroup per compute unit. Against a 256x128 tile at two workgroups per CU
+// this halves the global/L2 -> LDS traffic per flop (measured +4% of peak).
 // fp64: v_mfma_f64_16x16x4_f64, workgroup tile 128x128x16, each wave 64x64.
 //
-// Data path per K slice: global -> registers (prefetch of slice s+1 while
-// slice s is multiplied) -> LDS (double-buffered, one barrier per slice) ->
-// 16-byte LDS reads -> MFMA. LDS holds both operands k-contiguous: A as
-// [m][k] (a copy of a row-major tile) and B as [n][k] (each lane loads one
-// column's k values as scalars, so the transposition costs no shuffles). A
-// lane of MFMA lane group g = lane/16 then reads four consecutive k values
-// with one ds_read_b128 and feeds them to four MFMAs, i.e. MFMA number q
-// contracts k = {q, 4+q, 8+q, 12+q}; A and B use the same permutation, so
-// every product of the slice is summed exactly once.
+// Data path per K slice: global -> registers (prefetched ahead) -> LDS
+// (double-buffered, one barrier per slice) -> 16-byte LDS reads -> MFMA. LDS
+// holds both operands k-contiguous: A as [m][k] (a copy of a row-major tile)
+// and B as [n][k] (each lane loads one column's k values as scalars, so the
+// transposition costs no shuffles). A lane of MFMA lane group g = lane/16
+// then reads four consecutive k values with one ds_read_b128 and feeds them to
+// four MFMAs, i.e. MFMA number q contracts k = {q, 4+q, 8+q, 12+q}; A and B
+// use the same permutation, so every product of the slice is summed exactly
+// once.
 //
 // Schedule. Tiles are numbered batch-major and, inside a batch, in groups of
 // kGroupM tile rows, so neighbouring tiles share A and B panels. Whole rounds
@@ -24,13 +26,16 @@
 // slices over every resident slot (stream-K): a worker's run covers the end
 // of one tile and the start of the next, and every cut piece goes to a
 // workspace. A second kernel adds the pieces of each cut tile in K order, so
-// results are deterministic. Without this, e.g. 289 tiles on 512 slots leave
-// most compute units with one tile while 33 run two in sequence.
+// results are deterministic. Without this, e.g. 153 tiles on 256 compute units
+// leave 103 of them idle for the whole product.
 //
 // Modes: 0 = interior (no guards; M, N, K multiples of the tile and 16-byte
-// aligned rows), 1 = guarded vector loads of A (K % 4 == 0 for fp32, K even
-// for fp64), 2 = guarded scalar loads (any shape). Guarded loads fill zeros,
-// so edge tiles contract against +0 padding, and stores are masked.
+// aligned A rows), 1 = M/N edges (K a multiple of 16, aligned A rows): edge
+// rows and columns load clamped addresses and only the stores are masked,
+// since they feed no stored output; 2 = also a K edge with vector A loads
+// (K % 4 == 0 for fp32, K even for fp64), 3 = scalar loads (any shape). In
+// modes 2-3 loads past K read a clamped address and zero the value, so the
+// last slice contracts against +0 padding.
 //
 // Reference semantics: _gemm.py:24-137 (per-batch broadcast offsets
 // _offset :13-21, never reads C), _cuda.py:493-518 and :619-636.
@@ -94,21 +99,6 @@ __device__ __forceinline__ int64_t sk_worker(const Split& sp, int64_t g) {
   return g < long_runs ? g / (sp.base + 1) : sp.extra + (g - long_runs) / sp.base;
 }
 
-// First K slice of this workgroup's work and the end of it, both in the
-// concatenated slice space of its tile range; worker = -1 for whole tiles.
-__device__ __forceinline__ void work_range(const Split& sp, int64_t& g, int64_t& g_end, int64_t& worker) {
-  const int64_t bid = blockIdx.x;
-  if (bid < sp.dp_tiles) {
-    g = xcd_major(bid, sp.dp_tiles) * sp.slices;
-    g_end = g + sp.slices;
-    worker = -1;
-  } else {
-    worker = xcd_major(bid - sp.dp_tiles, sp.workers);
-    g = sp.dp_tiles * sp.slices + sk_begin(sp, worker);
-    g_end = sp.dp_tiles * sp.slices + sk_begin(sp, worker + 1);
-  }
-}
-
 __device__ __forceinline__ void batch_offsets(int64_t batch, const BatchDesc& bd, int64_t& a_off, int64_t& b_off) {
   a_off = 0;
   b_off = 0;
@@ -127,9 +117,9 @@ __device__ __forceinline__ void batch_offsets(int64_t batch, const BatchDesc& bd
 
 namespace f32 {
 
-constexpr int BM = 256, BN = 128, BK = 16;
+constexpr int BM = 256, BN = 256, BK = 16;
 constexpr int S = BK;  // LDS row stride (floats): 16-float rows, swizzled quads
-constexpr int kThreads = 256;
+constexpr int kThreads = 512;
 constexpr int FM = 8, FN = 4;  // MFMA blocks per wave
 constexpr int WM = 128, WN = 64;
 
@@ -140,33 +130,48 @@ constexpr int WM = 128, WN = 64;
 // distinct banks (measured: removes the LDS bank conflicts of padded rows).
 __device__ __forceinline__ int swizzle(int row) { return (row >> 1) & 3; }
 
-// Accumulator layout: lane holds column lane%16, rows 4*(lane/16) + r.
+// Eight waves in a 2x4 grid of 128x64 wave tiles. Accumulator layout: lane
+// holds column lane%16, rows 4*(lane/16) + r.
 struct Layout {
   static constexpr int kBM = BM, kBN = BN, kFM = FM, kFN = FN;
   static __device__ __forceinline__ int row(int wave, int i, int lane, int r) {
-    return (wave >> 1) * WM + 16 * i + 4 * (lane >> 4) + r;
+    return (wave >> 2) * WM + 16 * i + 4 * (lane >> 4) + r;
   }
-  static __device__ __forceinline__ int col(int wave, int j, int lane) { return (wave & 1) * WN + 16 * j + (lane & 15); }
+  static __device__ __forceinline__ int col(int wave, int j, int lane) { return (wave & 3) * WN + 16 * j + (lane & 15); }
 };
 
-template <int MODE>
-__global__ __launch_bounds__(kThreads, 2) void kernel(const float* __restrict__ A, const float* __restrict__ B,
+// One workgroup per compute unit (64 KB of LDS, 2 waves per SIMD). The
+// pipeline per K slice s:
+//   - global loads of slice s+2 into registers, issued first;
+//   - 128 MFMAs per wave on the fragments of slice s, already in registers;
+//     after the 16 MFMAs of A fragment i, that register is refilled with
+//     fragment i of slice s+1 from LDS (B fragments are double-buffered), so
+//     LDS reads overlap the matrix pipe instead of stalling each slice start;
+//   - after the MFMAs of fragment 5, slice s+2 goes from registers to the LDS
+//     buffer that held slice s (all waves read it during slice s-1);
+//   - one barrier.
+// STREAM_K = false: workgroup b computes whole tile xcd_major(b). true:
+// workgroup b is stream-K worker xcd_major(b) and computes its run, at most
+// the end of one tile and the start of the next (kept out of the whole-tile
+// kernel: the second inlined piece measurably slows the main loop).
+template <int MODE, bool STREAM_K>
+__global__ __launch_bounds__(kThreads, 1) void kernel(const float* __restrict__ A, const float* __restrict__ B,
                                                       float* __restrict__ C, int64_t M, int64_t N, int64_t K,
                                                       BatchDesc bd, TileMap tmap, Split sp) {
   __shared__ __attribute__((aligned(16))) float As[2][BM * S];
   __shared__ __attribute__((aligned(16))) float Bs[2][BN * S];
 
   const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
-  const int wm = wave >> 1, wn = wave & 1;
+  const int wm = wave >> 2, wn = wave & 3;
 
-  // Global -> register assignment. A: 4 float4 per thread (rows tid/4 + 64i,
-  // k quad tid%4). B: column n = tid%128, k quads 2*(tid/128) + {0, 1}
+  // Global -> register assignment. A: 2 float4 per thread (rows tid/4 + 128i,
+  // k quad tid%4). B: column n = tid%256, k quads 2*(tid/256) + {0, 1}
   // (8 scalar loads; 64 lanes read 256 contiguous bytes of one B row).
-  int a_row[4], a_lds[4];
+  int a_row[2], a_lds[2];
   const int a_kq = tid & 3;
 #pragma unroll
-  for (int i = 0; i < 4; ++i) {
-    a_row[i] = (tid >> 2) + 64 * i;
+  for (int i = 0; i < 2; ++i) {
+    a_row[i] = (tid >> 2) + 128 * i;
     a_lds[i] = a_row[i] * S + 4 * (a_kq ^ swizzle(a_row[i]));
   }
   const int b_n = tid & (BN - 1);
@@ -178,52 +183,60 @@ __global__ __launch_bounds__(kThreads, 2) void kernel(const float* __restrict__ 
   const int a_read = (wm * WM + (lane & 15)) * S + 4 * ((lane >> 4) ^ swizzle(lane & 15));
   const int b_read = (wn * WN + (lane & 15)) * S + 4 * ((lane >> 4) ^ swizzle(lane & 15));
 
-  int64_t run_begin, run_end, worker;
-  work_range(sp, run_begin, run_end, worker);
-  // One piece of K slices [g, g_end) inside one tile. Straight-line calls
-  // rather than a loop over pieces keep the register allocation of a single
-  // tile (a loop back-edge costs ~90 spilled registers).
-  auto piece = [&](int64_t g, int64_t g_end, bool first_piece) {
-    const int64_t tile = g / sp.slices;
-    const int64_t s0 = g - tile * sp.slices;
-    const int64_t s1 = s0 + (g_end - g);
+  // Tile `tile` over K slices [s0, s1). slot < 0: the piece is the whole K
+  // range and is stored to C; else it goes to workspace slot `slot`.
+  auto piece = [&](int64_t tile, int64_t s0, int64_t s1, int64_t slot) {
     int64_t batch, ti, tj;
     logical_tile(tile, tmap, batch, ti, tj);
     int64_t a_off, b_off;
     batch_offsets(batch, bd, a_off, b_off);
-    const float* Ab = A + a_off;
-    const float* Bb = B + b_off;
     const int64_t m0 = ti * BM, n0 = tj * BN;
+    // Operand origins at the piece's first k; kp = valid k extent from there.
+    const float* Ap = A + a_off + s0 * BK;
+    const float* Bp = B + b_off + s0 * BK * N;
+    const int64_t kp = K - s0 * BK;
+    const int64_t slices = s1 - s0;
 
-    hpd::f32x4 ra[4];
+    hpd::f32x4 ra[2];
     float rb[2][4];
 
     auto load_slice = [&](int64_t k0) {
 #pragma unroll
-      for (int i = 0; i < 4; ++i) {
+      for (int i = 0; i < 2; ++i) {
         const int64_t row = m0 + a_row[i];
         const int64_t kk = k0 + 4 * a_kq;
-        const float* p = Ab + row * K + kk;
-        if (MODE == 0) {
-          ra[i] = *reinterpret_cast<const hpd::f32x4*>(p);
-        } else if (MODE == 1) {
-          const bool ok = row < M && kk < K;
-          ra[i] = ok ? *reinterpret_cast<const hpd::f32x4*>(p) : hpd::f32x4{0.f, 0.f, 0.f, 0.f};
+        if (MODE <= 1) {
+          // Rows past M are clamped, not zeroed: they only feed output rows
+          // that are never stored.
+          ra[i] = *reinterpret_cast<const hpd::f32x4*>(Ap + (MODE == 0 || row < M ? row : M - 1) * K + kk);
         } else {
+          // K edge: a clamped in-bounds address and a zeroed value (branch
+          // free, unlike a guarded load).
+          const int64_t rc = row < M ? row : M - 1;
+          if (MODE == 2) {
+            const hpd::f32x4 v = *reinterpret_cast<const hpd::f32x4*>(Ap + rc * K + (kk < kp ? kk : kp - 4));
+            ra[i] = kk < kp ? v : hpd::f32x4{0.f, 0.f, 0.f, 0.f};
+          } else {
 #pragma unroll
-          for (int e = 0; e < 4; ++e) ra[i][e] = (row < M && kk + e < K) ? p[e] : 0.f;
+            for (int e = 0; e < 4; ++e) {
+              const float v = Ap[rc * K + (kk + e < kp ? kk + e : kp - 1)];
+              ra[i][e] = kk + e < kp ? v : 0.f;
+            }
+          }
         }
       }
-      const int64_t col = n0 + b_n;
+      // Columns past N are clamped likewise.
+      const int64_t col = MODE == 0 || n0 + b_n < N ? n0 + b_n : N - 1;
 #pragma unroll
       for (int q = 0; q < 2; ++q) {
 #pragma unroll
         for (int e = 0; e < 4; ++e) {
           const int64_t kr = k0 + 4 * (b_q + q) + e;
-          if (MODE == 0) {
-            rb[q][e] = Bb[kr * N + col];
+          if (MODE <= 1) {
+            rb[q][e] = Bp[kr * N + col];
           } else {
-            rb[q][e] = (kr < K && col < N) ? Bb[kr * N + col] : 0.f;
+            const float v = Bp[(kr < kp ? kr : kp - 1) * N + col];
+            rb[q][e] = kr < kp ? v : 0.f;
           }
         }
       }
@@ -231,7 +244,7 @@ __global__ __launch_bounds__(kThreads, 2) void kernel(const float* __restrict__ 
 
     auto store_slice = [&](int buf) {
 #pragma unroll
-      for (int i = 0; i < 4; ++i) *reinterpret_cast<hpd::f32x4*>(&As[buf][a_lds[i]]) = ra[i];
+      for (int i = 0; i < 2; ++i) *reinterpret_cast<hpd::f32x4*>(&As[buf][a_lds[i]]) = ra[i];
       *reinterpret_cast<hpd::f32x4*>(&Bs[buf][b_lds0]) = hpd::f32x4{rb[0][0], rb[0][1], rb[0][2], rb[0][3]};
       *reinterpret_cast<hpd::f32x4*>(&Bs[buf][b_lds1]) = hpd::f32x4{rb[1][0], rb[1][1], rb[1][2], rb[1][3]};
     };
@@ -242,31 +255,49 @@ __global__ __launch_bounds__(kThreads, 2) void kernel(const float* __restrict__ 
 #pragma unroll
       for (int j = 0; j < FN; ++j) acc[i][j] = hpd::f32x4{0.f, 0.f, 0.f, 0.f};
 
-    load_slice(s0 * BK);
+    load_slice(0);
     store_slice(0);
+    if (slices > 1) {
+      load_slice(BK);
+      store_slice(1);
+    }
     __syncthreads();
-    for (int64_t s = s0; s < s1; ++s) {
-      const int cur = int((s - s0) & 1);
-      if (s + 1 < s1) load_slice((s + 1) * BK);
-      hpd::f32x4 a[FM], b[FN];
+    hpd::f32x4 a[FM], b[FN], b_next[FN];
 #pragma unroll
-      for (int i = 0; i < FM; ++i) a[i] = *reinterpret_cast<const hpd::f32x4*>(&As[cur][a_read + 16 * i * S]);
+    for (int i = 0; i < FM; ++i) a[i] = *reinterpret_cast<const hpd::f32x4*>(&As[0][a_read + 16 * i * S]);
 #pragma unroll
-      for (int j = 0; j < FN; ++j) b[j] = *reinterpret_cast<const hpd::f32x4*>(&Bs[cur][b_read + 16 * j * S]);
+    for (int j = 0; j < FN; ++j) b[j] = *reinterpret_cast<const hpd::f32x4*>(&Bs[0][b_read + 16 * j * S]);
+    __syncthreads();  // every wave has read buffer 0 before slice 0 refills it
+    // Fragment read addresses of the next slice, carried across iterations:
+    // indexing As[(s + 1) & 1] directly lets the compiler rematerialize the
+    // address into each fragment register, and that write has to wait for
+    // the MFMAs still reading the register (measured: -3% of peak).
+    const float* a_src = &As[1][a_read];
+    const float* b_src = &Bs[1][b_read];
+    for (int64_t s = 0; s < slices; ++s) {
+      const bool more = s + 1 < slices;
+      if (s + 2 < slices) load_slice((s + 2) * BK);
 #pragma unroll
-      for (int q = 0; q < 4; ++q)
+      for (int i = 0; i < FM; ++i) {
 #pragma unroll
-        for (int i = 0; i < FM; ++i)
+        for (int q = 0; q < 4; ++q)
 #pragma unroll
           for (int j = 0; j < FN; ++j)
             acc[i][j] = __builtin_amdgcn_mfma_f32_16x16x4f32(a[i][q], b[j][q], acc[i][j], 0, 0, 0);
-      if (s + 1 < s1) store_slice(cur ^ 1);
-      // Also orders this piece's last LDS reads before the next piece's
-      // first LDS writes.
+        if (more) {
+          a[i] = *reinterpret_cast<const hpd::f32x4*>(a_src + 16 * i * S);
+          if (i >= FM - FN) b_next[i - (FM - FN)] = *reinterpret_cast<const hpd::f32x4*>(b_src + 16 * (i - (FM - FN)) * S);
+        }
+        if (i == 5 && s + 2 < slices) store_slice(int(s & 1));
+      }
+#pragma unroll
+      for (int j = 0; j < FN; ++j) b[j] = b_next[j];
+      a_src = (s & 1) ? &As[1][a_read] : &As[0][a_read];
+      b_src = (s & 1) ? &Bs[1][b_read] : &Bs[0][b_read];
       __syncthreads();
     }
 
-    if (s0 == 0 && s1 == sp.slices) {
+    if (slot < 0) {
       float* Cb = C + batch * M * N;
 #pragma unroll
       for (int i = 0; i < FM; ++i) {
@@ -281,20 +312,30 @@ __global__ __launch_bounds__(kThreads, 2) void kernel(const float* __restrict__ 
         }
       }
     } else {
-      // Cut piece: whole accumulator tile to the worker's workspace slot, in
-      // register order (16 contiguous bytes per lane).
-      hpd::f32x4* slot = static_cast<hpd::f32x4*>(sp.partial) + (worker * 2 + (first_piece ? 0 : 1)) * (BM * BN / 4);
+      // Cut piece: whole accumulator tile to the workspace slot, in register
+      // order (16 contiguous bytes per lane).
+      hpd::f32x4* out = static_cast<hpd::f32x4*>(sp.partial) + slot * (BM * BN / 4);
 #pragma unroll
       for (int i = 0; i < FM; ++i)
 #pragma unroll
-        for (int j = 0; j < FN; ++j) slot[((wave * FM + i) * FN + j) * 64 + lane] = acc[i][j];
+        for (int j = 0; j < FN; ++j) out[((wave * FM + i) * FN + j) * 64 + lane] = acc[i][j];
     }
   };
-  // A run is at most one tile long, so it covers the end of one tile and the
-  // start of the next at most.
-  const int64_t tile_end = (run_begin / sp.slices + 1) * sp.slices;
-  piece(run_begin, run_end < tile_end ? run_end : tile_end, true);
-  if (run_end > tile_end) piece(tile_end, run_end, false);
+
+  if (!STREAM_K) {
+    piece(xcd_major(blockIdx.x, sp.dp_tiles), 0, sp.slices, -1);
+  } else {
+    const int64_t worker = xcd_major(blockIdx.x, sp.workers);
+    const int64_t g = sk_begin(sp, worker), g_end = sk_begin(sp, worker + 1);
+    // A run is at most one tile long: the end of one tile and the start of
+    // the next at most.
+    const int64_t t0 = g / sp.slices;
+    const int64_t s0 = g - t0 * sp.slices;
+    const int64_t s1 = g_end - t0 * sp.slices < sp.slices ? g_end - t0 * sp.slices : sp.slices;
+    piece(sp.dp_tiles + t0, s0, s1, s0 == 0 && s1 == sp.slices ? -1 : worker * 2);
+    const int64_t rest = g_end - (t0 + 1) * sp.slices;
+    if (rest > 0) piece(sp.dp_tiles + t0 + 1, 0, rest, rest == sp.slices ? -1 : worker * 2 + 1);
+  }
 }
 
 }  // namespace f32
@@ -321,7 +362,8 @@ struct Layout {
   static __device__ __forceinline__ int col(int wave, int j, int lane) { return (wave & 1) * WN + 16 * j + (lane & 15); }
 };
 
-template <int MODE>
+// STREAM_K as for the fp32 kernel.
+template <int MODE, bool STREAM_K>
 __global__ __launch_bounds__(kThreads, 2) void kernel(const double* __restrict__ A, const double* __restrict__ B,
                                                       double* __restrict__ C, int64_t M, int64_t N, int64_t K,
                                                       BatchDesc bd, TileMap tmap, Split sp) {
@@ -344,22 +386,18 @@ __global__ __launch_bounds__(kThreads, 2) void kernel(const double* __restrict__
   const int a_read = (wm * WM + (lane & 15)) * SA + (lane >> 4) * 2;
   const int b_read = (wn * WN + (lane & 15)) * SB + (lane >> 4) * 2;
 
-  int64_t run_begin, run_end, worker;
-  work_range(sp, run_begin, run_end, worker);
-  // One piece of K slices [g, g_end) inside one tile. Straight-line calls
-  // rather than a loop over pieces keep the register allocation of a single
-  // tile (a loop back-edge costs ~90 spilled registers).
-  auto piece = [&](int64_t g, int64_t g_end, bool first_piece) {
-    const int64_t tile = g / sp.slices;
-    const int64_t s0 = g - tile * sp.slices;
-    const int64_t s1 = s0 + (g_end - g);
+  // Tile `tile` over K slices [s0, s1); slot < 0 stores to C, else to the
+  // workspace slot.
+  auto piece = [&](int64_t tile, int64_t s0, int64_t s1, int64_t slot) {
     int64_t batch, ti, tj;
     logical_tile(tile, tmap, batch, ti, tj);
     int64_t a_off, b_off;
     batch_offsets(batch, bd, a_off, b_off);
-    const double* Ab = A + a_off;
-    const double* Bb = B + b_off;
     const int64_t m0 = ti * BM, n0 = tj * BN;
+    const double* Ap = A + a_off + s0 * BK;
+    const double* Bp = B + b_off + s0 * BK * N;
+    const int64_t kp = K - s0 * BK;
+    const int64_t slices = s1 - s0;
 
     hpd::f64x2 ra[4];
     double rb[8];
@@ -369,25 +407,31 @@ __global__ __launch_bounds__(kThreads, 2) void kernel(const double* __restrict__
       for (int i = 0; i < 4; ++i) {
         const int64_t row = m0 + a_row[i];
         const int64_t kk = k0 + a_k;
-        const double* p = Ab + row * K + kk;
-        if (MODE == 0) {
-          ra[i] = *reinterpret_cast<const hpd::f64x2*>(p);
-        } else if (MODE == 1) {
-          const bool ok = row < M && kk < K;
-          ra[i] = ok ? *reinterpret_cast<const hpd::f64x2*>(p) : hpd::f64x2{0.0, 0.0};
+        if (MODE <= 1) {
+          ra[i] = *reinterpret_cast<const hpd::f64x2*>(Ap + (MODE == 0 || row < M ? row : M - 1) * K + kk);
         } else {
-          ra[i][0] = (row < M && kk < K) ? p[0] : 0.0;
-          ra[i][1] = (row < M && kk + 1 < K) ? p[1] : 0.0;
+          const int64_t rc = row < M ? row : M - 1;
+          if (MODE == 2) {
+            const hpd::f64x2 v = *reinterpret_cast<const hpd::f64x2*>(Ap + rc * K + (kk < kp ? kk : kp - 2));
+            ra[i] = kk < kp ? v : hpd::f64x2{0.0, 0.0};
+          } else {
+#pragma unroll
+            for (int e = 0; e < 2; ++e) {
+              const double v = Ap[rc * K + (kk + e < kp ? kk + e : kp - 1)];
+              ra[i][e] = kk + e < kp ? v : 0.0;
+            }
+          }
         }
       }
-      const int64_t col = n0 + b_n;
+      const int64_t col = MODE == 0 || n0 + b_n < N ? n0 + b_n : N - 1;
 #pragma unroll
       for (int s = 0; s < 8; ++s) {
         const int64_t kr = k0 + b_k + s;
-        if (MODE == 0) {
-          rb[s] = Bb[kr * N + col];
+        if (MODE <= 1) {
+          rb[s] = Bp[kr * N + col];
         } else {
-          rb[s] = (kr < K && col < N) ? Bb[kr * N + col] : 0.0;
+          const double v = Bp[(kr < kp ? kr : kp - 1) * N + col];
+          rb[s] = kr < kp ? v : 0.0;
         }
       }
     };
@@ -408,12 +452,12 @@ __global__ __launch_bounds__(kThreads, 2) void kernel(const double* __restrict__
 #pragma unroll
       for (int j = 0; j < FN; ++j) acc[i][j] = f64x4{0.0, 0.0, 0.0, 0.0};
 
-    load_slice(s0 * BK);
+    load_slice(0);
     store_slice(0);
     __syncthreads();
-    for (int64_t s = s0; s < s1; ++s) {
-      const int cur = int((s - s0) & 1);
-      if (s + 1 < s1) load_slice((s + 1) * BK);
+    for (int64_t s = 0; s < slices; ++s) {
+      const int cur = int(s & 1);
+      if (s + 1 < slices) load_slice((s + 1) * BK);
 #pragma unroll
       for (int half = 0; half < 2; ++half) {
         hpd::f64x2 a[FM], b[FN];
@@ -431,11 +475,11 @@ __global__ __launch_bounds__(kThreads, 2) void kernel(const double* __restrict__
             for (int j = 0; j < FN; ++j)
               acc[i][j] = __builtin_amdgcn_mfma_f64_16x16x4f64(a[i][q], b[j][q], acc[i][j], 0, 0, 0);
       }
-      if (s + 1 < s1) store_slice(cur ^ 1);
+      if (s + 1 < slices) store_slice(cur ^ 1);
       __syncthreads();
     }
 
-    if (s0 == 0 && s1 == sp.slices) {
+    if (slot < 0) {
       double* Cb = C + batch * M * N;
 #pragma unroll
       for (int i = 0; i < FM; ++i) {
@@ -450,18 +494,26 @@ __global__ __launch_bounds__(kThreads, 2) void kernel(const double* __restrict__
         }
       }
     } else {
-      f64x4* slot = static_cast<f64x4*>(sp.partial) + (worker * 2 + (first_piece ? 0 : 1)) * (BM * BN / 4);
+      f64x4* out = static_cast<f64x4*>(sp.partial) + slot * (BM * BN / 4);
 #pragma unroll
       for (int i = 0; i < FM; ++i)
 #pragma unroll
-        for (int j = 0; j < FN; ++j) slot[((wave * FM + i) * FN + j) * 64 + lane] = acc[i][j];
+        for (int j = 0; j < FN; ++j) out[((wave * FM + i) * FN + j) * 64 + lane] = acc[i][j];
     }
   };
-  // A run is at most one tile long, so it covers the end of one tile and the
-  // start of the next at most.
-  const int64_t tile_end = (run_begin / sp.slices + 1) * sp.slices;
-  piece(run_begin, run_end < tile_end ? run_end : tile_end, true);
-  if (run_end > tile_end) piece(tile_end, run_end, false);
+
+  if (!STREAM_K) {
+    piece(xcd_major(blockIdx.x, sp.dp_tiles), 0, sp.slices, -1);
+  } else {
+    const int64_t worker = xcd_major(blockIdx.x, sp.workers);
+    const int64_t g = sk_begin(sp, worker), g_end = sk_begin(sp, worker + 1);
+    const int64_t t0 = g / sp.slices;
+    const int64_t s0 = g - t0 * sp.slices;
+    const int64_t s1 = g_end - t0 * sp.slices < sp.slices ? g_end - t0 * sp.slices : sp.slices;
+    piece(sp.dp_tiles + t0, s0, s1, s0 == 0 && s1 == sp.slices ? -1 : worker * 2);
+    const int64_t rest = g_end - (t0 + 1) * sp.slices;
+    if (rest > 0) piece(sp.dp_tiles + t0 + 1, 0, rest, rest == sp.slices ? -1 : worker * 2 + 1);
+  }
 }
 
 }  // namespace f64
@@ -526,11 +578,19 @@ bool a_strides_aligned(const BatchDesc& bd, int64_t elems_per_16b) {
   return true;
 }
 
+// Workgroups of `kernel` resident per compute unit, queried once per kernel.
 template <typename F>
 int resident_per_cu(F kernel, int threads) {
+  static std::mutex mutex;
+  static std::unordered_map<const void*, int> known;
+  const void* key = reinterpret_cast<const void*>(kernel);
+  std::lock_guard<std::mutex> lock(mutex);
+  auto it = known.find(key);
+  if (it != known.end()) return it->second;
   int blocks = 0;
   HP_CHECK(hipOccupancyMaxActiveBlocksPerMultiprocessor(&blocks, kernel, threads, 0));
   hp::require(blocks > 0, "GEMM kernel does not fit on a compute unit");
+  known.emplace(key, blocks);
   return blocks;
 }
 
@@ -555,21 +615,23 @@ Split plan_split(int64_t total, int64_t slices, int64_t slots) {
   return sp;
 }
 
-// Launches kernel (grid = whole tiles + stream-K workers) and, if tiles were
-// cut, the fixup over a pooled workspace.
-template <typename T, int BM, int BN, typename Main, typename Fix>
-void launch_split(hp_ctx* ctx, Main main, Fix fixup, int per_cu, int threads, const T* a, const T* b, T* c,
+// Launches the whole-tile kernel over the complete rounds and, if tiles are
+// cut, the stream-K kernel and the fixup over a pooled workspace.
+template <typename T, int BM, int BN, typename Whole, typename Cut, typename Fix>
+void launch_split(hp_ctx* ctx, Whole whole, Cut cut, Fix fixup, int threads, const T* a, const T* b, T* c,
                   int64_t m, int64_t n, int64_t k, const BatchDesc& bd, const TileMap& tm, int64_t bk,
                   const char* name) {
+  const int per_cu = std::min(resident_per_cu(whole, threads), resident_per_cu(cut, threads));
   Split sp = plan_split(tm.total, hp::ceil_div(k, bk), int64_t(ctx->compute_units) * per_cu);
+  if (sp.dp_tiles > 0) {
+    whole<<<sp.dp_tiles, threads, 0, ctx->stream>>>(a, b, c, m, n, k, bd, tm, sp);
+    hp::check_launch(name);
+  }
   if (sp.workers > 0) {
     sp.partial = hp::scratch_alloc(ctx, size_t(sp.workers) * 2 * BM * BN * sizeof(T));
-  }
-  main<<<sp.dp_tiles + sp.workers, threads, 0, ctx->stream>>>(a, b, c, m, n, k, bd, tm, sp);
-  hp::check_launch(name);
-  if (sp.workers > 0) {
-    const int64_t cut = tm.total - sp.dp_tiles;
-    fixup<<<cut * (BM * BN / 4 / 256), 256, 0, ctx->stream>>>(c, m, n, tm, sp);
+    cut<<<sp.workers, threads, 0, ctx->stream>>>(a, b, c, m, n, k, bd, tm, sp);
+    hp::check_launch(name);
+    fixup<<<(tm.total - sp.dp_tiles) * (BM * BN / 4 / 256), 256, 0, ctx->stream>>>(c, m, n, tm, sp);
     hp::check_launch(name);
     hp::scratch_free(ctx, sp.partial);
   }
@@ -581,17 +643,19 @@ void run_f32(hp_ctx* ctx, const float* a, const float* b, float* c, int64_t m, i
   TileMap tm;
   prepare(m, n, batch, BM, BN, tm);
   const bool vec_ok = aligned16(a) && k % 4 == 0 && a_strides_aligned(bd, 4);
-  const bool interior = vec_ok && m % BM == 0 && n % BN == 0 && k % BK == 0;
   auto fix = fixup_kernel<float, hpd::f32x4, Layout>;
-  static const int occ0 = resident_per_cu(kernel<0>, kThreads);
-  static const int occ1 = resident_per_cu(kernel<1>, kThreads);
-  static const int occ2 = resident_per_cu(kernel<2>, kThreads);
-  if (interior) {
-    launch_split<float, BM, BN>(ctx, kernel<0>, fix, occ0, kThreads, a, b, c, m, n, k, bd, tm, BK, "gemm_f32");
+  if (vec_ok && k % BK == 0 && m % BM == 0 && n % BN == 0) {
+    launch_split<float, BM, BN>(ctx, kernel<0, false>, kernel<0, true>, fix, kThreads, a, b, c, m, n, k, bd, tm, BK,
+                                "gemm_f32");
+  } else if (vec_ok && k % BK == 0) {
+    launch_split<float, BM, BN>(ctx, kernel<1, false>, kernel<1, true>, fix, kThreads, a, b, c, m, n, k, bd, tm, BK,
+                                "gemm_f32");
   } else if (vec_ok) {
-    launch_split<float, BM, BN>(ctx, kernel<1>, fix, occ1, kThreads, a, b, c, m, n, k, bd, tm, BK, "gemm_f32");
+    launch_split<float, BM, BN>(ctx, kernel<2, false>, kernel<2, true>, fix, kThreads, a, b, c, m, n, k, bd, tm, BK,
+                                "gemm_f32");
   } else {
-    launch_split<float, BM, BN>(ctx, kernel<2>, fix, occ2, kThreads, a, b, c, m, n, k, bd, tm, BK, "gemm_f32");
+    launch_split<float, BM, BN>(ctx, kernel<3, false>, kernel<3, true>, fix, kThreads, a, b, c, m, n, k, bd, tm, BK,
+                                "gemm_f32");
   }
 }
 
@@ -601,17 +665,19 @@ void run_f64(hp_ctx* ctx, const double* a, const double* b, double* c, int64_t m
   TileMap tm;
   prepare(m, n, batch, BM, BN, tm);
   const bool vec_ok = aligned16(a) && k % 2 == 0 && a_strides_aligned(bd, 2);
-  const bool interior = vec_ok && m % BM == 0 && n % BN == 0 && k % BK == 0;
   auto fix = fixup_kernel<double, f64x4, Layout>;
-  static const int occ0 = resident_per_cu(kernel<0>, kThreads);
-  static const int occ1 = resident_per_cu(kernel<1>, kThreads);
-  static const int occ2 = resident_per_cu(kernel<2>, kThreads);
-  if (interior) {
-    launch_split<double, BM, BN>(ctx, kernel<0>, fix, occ0, kThreads, a, b, c, m, n, k, bd, tm, BK, "gemm_f64");
+  if (vec_ok && k % BK == 0 && m % BM == 0 && n % BN == 0) {
+    launch_split<double, BM, BN>(ctx, kernel<0, false>, kernel<0, true>, fix, kThreads, a, b, c, m, n, k, bd, tm, BK,
+                                 "gemm_f64");
+  } else if (vec_ok && k % BK == 0) {
+    launch_split<double, BM, BN>(ctx, kernel<1, false>, kernel<1, true>, fix, kThreads, a, b, c, m, n, k, bd, tm, BK,
+                                 "gemm_f64");
   } else if (vec_ok) {
-    launch_split<double, BM, BN>(ctx, kernel<1>, fix, occ1, kThreads, a, b, c, m, n, k, bd, tm, BK, "gemm_f64");
+    launch_split<double, BM, BN>(ctx, kernel<2, false>, kernel<2, true>, fix, kThreads, a, b, c, m, n, k, bd, tm, BK,
+                                 "gemm_f64");
   } else {
-    launch_split<double, BM, BN>(ctx, kernel<2>, fix, occ2, kThreads, a, b, c, m, n, k, bd, tm, BK, "gemm_f64");
+    launch_split<double, BM, BN>(ctx, kernel<3, false>, kernel<3, true>, fix, kThreads, a, b, c, m, n, k, bd, tm, BK,
+                                 "gemm_f64");
   }
 }
 

@@ -22,7 +22,7 @@ from math import prod
 import numpy as np
 
 ALIGNMENT = (32, 16, 32)  # M, K, N (reference explain() field)
-KERNEL_TILE = (256, 16, 128)  # M, K, N workgroup tile of the fp32 MFMA GEMM
+KERNEL_TILE = (256, 16, 256)  # M, K, N workgroup tile of the fp32 MFMA GEMM
 
 
 def _round_up(value, multiple):
