@@ -5,7 +5,8 @@
 // grid, each wave 128x64 (8x4 MFMA blocks, 128 accumulators per lane); one
 // workgroup per compute unit. Against a 256x128 tile at two workgroups per CU
 // this halves the global/L2 -> LDS traffic per flop (measured +4% of peak).
-// fp64: v_mfma_f64_16x16x4_f64, workgroup tile 128x128x16, each wave 64x64.
+// fp64: v_mfma_f64_16x16x4_f64, workgroup tile 256x128x16, eight waves in a
+// 4x2 grid of 64x64 wave tiles, one workgroup per compute unit.
 //
 // Data path per K slice: global -> registers (prefetched ahead) -> LDS
 // (double-buffered, one barrier per slice) -> 16-byte LDS reads -> MFMA. LDS
@@ -344,16 +345,22 @@ __global__ __launch_bounds__(kThreads, 1) void kernel(const float* __restrict__ 
 
 namespace f64 {
 
-constexpr int BM = 128, BN = 128, BK = 16;
-constexpr int SA = BK + 2;  // LDS row stride in doubles
-constexpr int SB = BK + 2;
-constexpr int kThreads = 256;
+constexpr int BM = 256, BN = 128, BK = 16;
+constexpr int S = BK;  // LDS row stride (doubles): 8 swizzled k pairs of 16 bytes
+constexpr int kThreads = 512;
 constexpr int FM = 4, FN = 4;
 constexpr int WM = 64, WN = 64;
 
 typedef double f64x4 __attribute__((ext_vector_type(4)));
 
-// f64 accumulator layout: lane holds column lane%16, rows 4*r + lane/16.
+// LDS rows hold 8 pairs of consecutive k values; pair p of row r is stored at
+// slot p ^ ((r >> 1) & 7). Rows are 128 bytes, so 16 lanes reading one pair of
+// rows r0..r0+15 (fragment reads), writing 8 pairs of 2 rows (A stores) or one
+// pair of 16 rows (B stores) touch 16 distinct 16-byte bank groups.
+__device__ __forceinline__ int swizzle(int row) { return (row >> 1) & 7; }
+
+// Eight waves in a 4x2 grid of 64x64 wave tiles. f64 accumulator layout: lane
+// holds column lane%16, rows 4*r + lane/16.
 struct Layout {
   static constexpr int kBM = BM, kBN = BN, kFM = FM, kFN = FN;
   static __device__ __forceinline__ int row(int wave, int i, int lane, int r) {
@@ -362,32 +369,42 @@ struct Layout {
   static __device__ __forceinline__ int col(int wave, int j, int lane) { return (wave & 1) * WN + 16 * j + (lane & 15); }
 };
 
-// STREAM_K as for the fp32 kernel.
+// One workgroup per compute unit, the pipeline of the fp32 kernel: per slice,
+// global loads of slice s+2 first; MFMAs of slice s in two k halves of 8,
+// each A fragment refilled from LDS with slice s+1 right after its MFMAs and
+// the B fragments of a half after that half; slice s+2 to LDS after half 0;
+// one barrier. A lane of MFMA lane group g = lane/16 reads the k pair
+// {2g, 2g+1} (half 0) or {8+2g, 9+2g} (half 1) with one ds_read_b128 and
+// feeds it to two MFMAs (k-permutation shared by A and B).
 template <int MODE, bool STREAM_K>
-__global__ __launch_bounds__(kThreads, 2) void kernel(const double* __restrict__ A, const double* __restrict__ B,
+__global__ __launch_bounds__(kThreads, 1) void kernel(const double* __restrict__ A, const double* __restrict__ B,
                                                       double* __restrict__ C, int64_t M, int64_t N, int64_t K,
                                                       BatchDesc bd, TileMap tmap, Split sp) {
-  __shared__ __attribute__((aligned(16))) double As[2][BM * SA];
-  __shared__ __attribute__((aligned(16))) double Bs[2][BN * SB];
+  __shared__ __attribute__((aligned(16))) double As[2][BM * S];
+  __shared__ __attribute__((aligned(16))) double Bs[2][BN * S];
 
   const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
   const int wm = wave >> 1, wn = wave & 1;
 
-  // A: 4 double2 per thread (rows tid/8 + 32i, k pair tid%8).
-  // B: column n = tid%128, k rows 8*(tid/128) + {0..7} (8 scalar loads).
+  // A: 4 double2 per thread (rows tid/8 + 64i, k pair tid%8). B: column
+  // n = tid%128, k rows 4*(tid/128) + {0..3} (4 scalar loads; 64 lanes read
+  // 512 contiguous bytes of one B row), stored as 2 pairs.
   int a_row[4];
-  const int a_k = (tid & 7) * 2;
+  const int a_pair = tid & 7;
 #pragma unroll
-  for (int i = 0; i < 4; ++i) a_row[i] = (tid >> 3) + 32 * i;
-  const int b_n = tid & 127;
-  const int b_k = (tid >> 7) * 8;
-  // Lane group g = lane/16 reads k = 2g, 2g+1 (first half of the slice) and
-  // 8 + 2g, 8 + 2g + 1 (second half): MFMA q in {0,1} per half.
-  const int a_read = (wm * WM + (lane & 15)) * SA + (lane >> 4) * 2;
-  const int b_read = (wn * WN + (lane & 15)) * SB + (lane >> 4) * 2;
+  for (int i = 0; i < 4; ++i) a_row[i] = (tid >> 3) + 64 * i;
+  const int a_lds = a_row[0] * S + 2 * (a_pair ^ swizzle(a_row[0]));  // + i * 64 * S
+  const int b_n = tid & (BN - 1);
+  const int b_p = (tid / BN) * 2;
+  const int b_lds0 = b_n * S + 2 * (b_p ^ swizzle(b_n));
+  const int b_lds1 = b_n * S + 2 * ((b_p + 1) ^ swizzle(b_n));
+  // Fragment rows differ from (lane & 15) by multiples of 16: same swizzle.
+  const int sw = swizzle(lane & 15), g = lane >> 4;
+  const int a_read0 = (wm * WM + (lane & 15)) * S + 2 * (g ^ sw);
+  const int a_read1 = (wm * WM + (lane & 15)) * S + 2 * ((4 + g) ^ sw);
+  const int b_read0 = (wn * WN + (lane & 15)) * S + 2 * (g ^ sw);
+  const int b_read1 = (wn * WN + (lane & 15)) * S + 2 * ((4 + g) ^ sw);
 
-  // Tile `tile` over K slices [s0, s1); slot < 0 stores to C, else to the
-  // workspace slot.
   auto piece = [&](int64_t tile, int64_t s0, int64_t s1, int64_t slot) {
     int64_t batch, ti, tj;
     logical_tile(tile, tmap, batch, ti, tj);
@@ -400,13 +417,13 @@ __global__ __launch_bounds__(kThreads, 2) void kernel(const double* __restrict__
     const int64_t slices = s1 - s0;
 
     hpd::f64x2 ra[4];
-    double rb[8];
+    double rb[4];
 
     auto load_slice = [&](int64_t k0) {
 #pragma unroll
       for (int i = 0; i < 4; ++i) {
         const int64_t row = m0 + a_row[i];
-        const int64_t kk = k0 + a_k;
+        const int64_t kk = k0 + 2 * a_pair;
         if (MODE <= 1) {
           ra[i] = *reinterpret_cast<const hpd::f64x2*>(Ap + (MODE == 0 || row < M ? row : M - 1) * K + kk);
         } else {
@@ -425,25 +442,22 @@ __global__ __launch_bounds__(kThreads, 2) void kernel(const double* __restrict__
       }
       const int64_t col = MODE == 0 || n0 + b_n < N ? n0 + b_n : N - 1;
 #pragma unroll
-      for (int s = 0; s < 8; ++s) {
-        const int64_t kr = k0 + b_k + s;
+      for (int e = 0; e < 4; ++e) {
+        const int64_t kr = k0 + 2 * b_p + e;
         if (MODE <= 1) {
-          rb[s] = Bp[kr * N + col];
+          rb[e] = Bp[kr * N + col];
         } else {
           const double v = Bp[(kr < kp ? kr : kp - 1) * N + col];
-          rb[s] = kr < kp ? v : 0.0;
+          rb[e] = kr < kp ? v : 0.0;
         }
       }
     };
 
     auto store_slice = [&](int buf) {
 #pragma unroll
-      for (int i = 0; i < 4; ++i) *reinterpret_cast<hpd::f64x2*>(&As[buf][a_row[i] * SA + a_k]) = ra[i];
-#pragma unroll
-      for (int s = 0; s < 4; ++s) {
-        const hpd::f64x2 v = {rb[2 * s], rb[2 * s + 1]};
-        *reinterpret_cast<hpd::f64x2*>(&Bs[buf][b_n * SB + b_k + 2 * s]) = v;
-      }
+      for (int i = 0; i < 4; ++i) *reinterpret_cast<hpd::f64x2*>(&As[buf][a_lds + i * 64 * S]) = ra[i];
+      *reinterpret_cast<hpd::f64x2*>(&Bs[buf][b_lds0]) = hpd::f64x2{rb[0], rb[1]};
+      *reinterpret_cast<hpd::f64x2*>(&Bs[buf][b_lds1]) = hpd::f64x2{rb[2], rb[3]};
     };
 
     f64x4 acc[FM][FN];
@@ -454,28 +468,50 @@ __global__ __launch_bounds__(kThreads, 2) void kernel(const double* __restrict__
 
     load_slice(0);
     store_slice(0);
+    if (slices > 1) {
+      load_slice(BK);
+      store_slice(1);
+    }
     __syncthreads();
+    hpd::f64x2 a[2][FM], b[2][FN];
+#pragma unroll
+    for (int i = 0; i < FM; ++i) {
+      a[0][i] = *reinterpret_cast<const hpd::f64x2*>(&As[0][a_read0 + 16 * i * S]);
+      a[1][i] = *reinterpret_cast<const hpd::f64x2*>(&As[0][a_read1 + 16 * i * S]);
+    }
+#pragma unroll
+    for (int j = 0; j < FN; ++j) {
+      b[0][j] = *reinterpret_cast<const hpd::f64x2*>(&Bs[0][b_read0 + 16 * j * S]);
+      b[1][j] = *reinterpret_cast<const hpd::f64x2*>(&Bs[0][b_read1 + 16 * j * S]);
+    }
+    __syncthreads();  // every wave has read buffer 0 before slice 0 refills it
+    // Next-slice LDS buffers, carried across iterations (see the fp32 kernel).
+    const double* a_src = As[1];
+    const double* b_src = Bs[1];
     for (int64_t s = 0; s < slices; ++s) {
-      const int cur = int(s & 1);
-      if (s + 1 < slices) load_slice((s + 1) * BK);
+      const bool more = s + 1 < slices;
+      if (s + 2 < slices) load_slice((s + 2) * BK);
 #pragma unroll
-      for (int half = 0; half < 2; ++half) {
-        hpd::f64x2 a[FM], b[FN];
+      for (int h = 0; h < 2; ++h) {
+        const int a_read = h == 0 ? a_read0 : a_read1;
+        const int b_read = h == 0 ? b_read0 : b_read1;
 #pragma unroll
-        for (int i = 0; i < FM; ++i)
-          a[i] = *reinterpret_cast<const hpd::f64x2*>(&As[cur][a_read + 16 * i * SA + 8 * half]);
+        for (int i = 0; i < FM; ++i) {
 #pragma unroll
-        for (int j = 0; j < FN; ++j)
-          b[j] = *reinterpret_cast<const hpd::f64x2*>(&Bs[cur][b_read + 16 * j * SB + 8 * half]);
-#pragma unroll
-        for (int q = 0; q < 2; ++q)
-#pragma unroll
-          for (int i = 0; i < FM; ++i)
+          for (int q = 0; q < 2; ++q)
 #pragma unroll
             for (int j = 0; j < FN; ++j)
-              acc[i][j] = __builtin_amdgcn_mfma_f64_16x16x4f64(a[i][q], b[j][q], acc[i][j], 0, 0, 0);
+              acc[i][j] = __builtin_amdgcn_mfma_f64_16x16x4f64(a[h][i][q], b[h][j][q], acc[i][j], 0, 0, 0);
+          if (more) a[h][i] = *reinterpret_cast<const hpd::f64x2*>(a_src + a_read + 16 * i * S);
+        }
+        if (more) {
+#pragma unroll
+          for (int j = 0; j < FN; ++j) b[h][j] = *reinterpret_cast<const hpd::f64x2*>(b_src + b_read + 16 * j * S);
+        }
+        if (h == 0 && s + 2 < slices) store_slice(int(s & 1));
       }
-      if (s + 1 < slices) store_slice(cur ^ 1);
+      a_src = (s & 1) ? As[1] : As[0];
+      b_src = (s & 1) ? Bs[1] : Bs[0];
       __syncthreads();
     }
 
@@ -506,9 +542,9 @@ __global__ __launch_bounds__(kThreads, 2) void kernel(const double* __restrict__
     piece(xcd_major(blockIdx.x, sp.dp_tiles), 0, sp.slices, -1);
   } else {
     const int64_t worker = xcd_major(blockIdx.x, sp.workers);
-    const int64_t g = sk_begin(sp, worker), g_end = sk_begin(sp, worker + 1);
-    const int64_t t0 = g / sp.slices;
-    const int64_t s0 = g - t0 * sp.slices;
+    const int64_t g0 = sk_begin(sp, worker), g_end = sk_begin(sp, worker + 1);
+    const int64_t t0 = g0 / sp.slices;
+    const int64_t s0 = g0 - t0 * sp.slices;
     const int64_t s1 = g_end - t0 * sp.slices < sp.slices ? g_end - t0 * sp.slices : sp.slices;
     piece(sp.dp_tiles + t0, s0, s1, s0 == 0 && s1 == sp.slices ? -1 : worker * 2);
     const int64_t rest = g_end - (t0 + 1) * sp.slices;
