@@ -30,13 +30,12 @@
 // results are deterministic. Without this, e.g. 153 tiles on 256 compute units
 // leave 103 of them idle for the whole product.
 //
-// Modes: 0 = interior (no guards; M, N, K multiples of the tile and 16-byte
-// aligned A rows), 1 = M/N edges (K a multiple of 16, aligned A rows): edge
-// rows and columns load clamped addresses and only the stores are masked,
-// since they feed no stored output; 2 = also a K edge with vector A loads
-// (K % 4 == 0 for fp32, K even for fp64), 3 = scalar loads (any shape). In
-// modes 2-3 loads past K read a clamped address and zero the value, so the
-// last slice contracts against +0 padding.
+// Modes: 0 = interior (no guards; M, N, K multiples of the tile), 1 = M/N
+// edges (K a multiple of 16): edge rows and columns load clamped addresses
+// and only the stores are masked, since they feed no stored output; 2 = any
+// K: as 1, plus the one slice holding the K edge takes scalar loads that
+// zero-fill past K, so it contracts against +0 padding. A rows are read as
+// 16-byte vectors at element alignment (odd K included).
 //
 // Reference semantics: _gemm.py:24-137 (per-batch broadcast offsets
 // _offset :13-21, never reads C), _cuda.py:493-518 and :619-636.
@@ -70,6 +69,11 @@ struct Split {
 };
 
 constexpr int64_t kGroupM = 8;
+
+// 16-byte operand loads that need only element alignment (rows of an odd K
+// or a view at any element offset): one global_load_dwordx4 all the same.
+typedef float f32x4u __attribute__((ext_vector_type(4), aligned(4)));
+typedef double f64x2u __attribute__((ext_vector_type(2), aligned(8)));
 constexpr int64_t kMinSlices = 8;  // shortest stream-K run
 
 __device__ __forceinline__ void logical_tile(int64_t t, const TileMap& tm, int64_t& batch, int64_t& ti,
@@ -201,46 +205,40 @@ __global__ __launch_bounds__(kThreads, 1) void kernel(const float* __restrict__ 
     hpd::f32x4 ra[2];
     float rb[2][4];
 
+    // Rows past M and columns past N load clamped addresses and are not
+    // zeroed: they only feed outputs that are never stored. In mode 2 the
+    // slice holding the K edge (uniform test) takes scalar loads, zero past K.
+    const int64_t a_col0 = 4 * a_kq;
+    const int64_t b_col = MODE == 0 || n0 + b_n < N ? n0 + b_n : N - 1;
     auto load_slice = [&](int64_t k0) {
+      if (MODE == 2 && k0 + BK > kp) {
+#pragma unroll
+        for (int i = 0; i < 2; ++i) {
+          const int64_t row = m0 + a_row[i] < M ? m0 + a_row[i] : M - 1;
+#pragma unroll
+          for (int e = 0; e < 4; ++e) {
+            const int64_t kk = k0 + a_col0 + e;
+            ra[i][e] = kk < kp ? Ap[row * K + kk] : 0.f;
+          }
+        }
+#pragma unroll
+        for (int q = 0; q < 2; ++q)
+#pragma unroll
+          for (int e = 0; e < 4; ++e) {
+            const int64_t kr = k0 + 4 * (b_q + q) + e;
+            rb[q][e] = kr < kp ? Bp[kr * N + b_col] : 0.f;
+          }
+        return;
+      }
 #pragma unroll
       for (int i = 0; i < 2; ++i) {
-        const int64_t row = m0 + a_row[i];
-        const int64_t kk = k0 + 4 * a_kq;
-        if (MODE <= 1) {
-          // Rows past M are clamped, not zeroed: they only feed output rows
-          // that are never stored.
-          ra[i] = *reinterpret_cast<const hpd::f32x4*>(Ap + (MODE == 0 || row < M ? row : M - 1) * K + kk);
-        } else {
-          // K edge: a clamped in-bounds address and a zeroed value (branch
-          // free, unlike a guarded load).
-          const int64_t rc = row < M ? row : M - 1;
-          if (MODE == 2) {
-            const hpd::f32x4 v = *reinterpret_cast<const hpd::f32x4*>(Ap + rc * K + (kk < kp ? kk : kp - 4));
-            ra[i] = kk < kp ? v : hpd::f32x4{0.f, 0.f, 0.f, 0.f};
-          } else {
-#pragma unroll
-            for (int e = 0; e < 4; ++e) {
-              const float v = Ap[rc * K + (kk + e < kp ? kk + e : kp - 1)];
-              ra[i][e] = kk + e < kp ? v : 0.f;
-            }
-          }
-        }
+        const int64_t row = MODE == 0 || m0 + a_row[i] < M ? m0 + a_row[i] : M - 1;
+        ra[i] = *reinterpret_cast<const f32x4u*>(Ap + row * K + k0 + a_col0);
       }
-      // Columns past N are clamped likewise.
-      const int64_t col = MODE == 0 || n0 + b_n < N ? n0 + b_n : N - 1;
 #pragma unroll
-      for (int q = 0; q < 2; ++q) {
+      for (int q = 0; q < 2; ++q)
 #pragma unroll
-        for (int e = 0; e < 4; ++e) {
-          const int64_t kr = k0 + 4 * (b_q + q) + e;
-          if (MODE <= 1) {
-            rb[q][e] = Bp[kr * N + col];
-          } else {
-            const float v = Bp[(kr < kp ? kr : kp - 1) * N + col];
-            rb[q][e] = kr < kp ? v : 0.f;
-          }
-        }
-      }
+        for (int e = 0; e < 4; ++e) rb[q][e] = Bp[(k0 + 4 * (b_q + q) + e) * N + b_col];
     };
 
     auto store_slice = [&](int buf) {
@@ -419,38 +417,34 @@ __global__ __launch_bounds__(kThreads, 1) void kernel(const double* __restrict__
     hpd::f64x2 ra[4];
     double rb[4];
 
+    // Edge handling as in the fp32 kernel.
+    const int64_t a_col0 = 2 * a_pair;
+    const int64_t b_col = MODE == 0 || n0 + b_n < N ? n0 + b_n : N - 1;
     auto load_slice = [&](int64_t k0) {
+      if (MODE == 2 && k0 + BK > kp) {
 #pragma unroll
-      for (int i = 0; i < 4; ++i) {
-        const int64_t row = m0 + a_row[i];
-        const int64_t kk = k0 + 2 * a_pair;
-        if (MODE <= 1) {
-          ra[i] = *reinterpret_cast<const hpd::f64x2*>(Ap + (MODE == 0 || row < M ? row : M - 1) * K + kk);
-        } else {
-          const int64_t rc = row < M ? row : M - 1;
-          if (MODE == 2) {
-            const hpd::f64x2 v = *reinterpret_cast<const hpd::f64x2*>(Ap + rc * K + (kk < kp ? kk : kp - 2));
-            ra[i] = kk < kp ? v : hpd::f64x2{0.0, 0.0};
-          } else {
+        for (int i = 0; i < 4; ++i) {
+          const int64_t row = m0 + a_row[i] < M ? m0 + a_row[i] : M - 1;
 #pragma unroll
-            for (int e = 0; e < 2; ++e) {
-              const double v = Ap[rc * K + (kk + e < kp ? kk + e : kp - 1)];
-              ra[i][e] = kk + e < kp ? v : 0.0;
-            }
+          for (int e = 0; e < 2; ++e) {
+            const int64_t kk = k0 + a_col0 + e;
+            ra[i][e] = kk < kp ? Ap[row * K + kk] : 0.0;
           }
         }
-      }
-      const int64_t col = MODE == 0 || n0 + b_n < N ? n0 + b_n : N - 1;
 #pragma unroll
-      for (int e = 0; e < 4; ++e) {
-        const int64_t kr = k0 + 2 * b_p + e;
-        if (MODE <= 1) {
-          rb[e] = Bp[kr * N + col];
-        } else {
-          const double v = Bp[(kr < kp ? kr : kp - 1) * N + col];
-          rb[e] = kr < kp ? v : 0.0;
+        for (int e = 0; e < 4; ++e) {
+          const int64_t kr = k0 + 2 * b_p + e;
+          rb[e] = kr < kp ? Bp[kr * N + b_col] : 0.0;
         }
+        return;
       }
+#pragma unroll
+      for (int i = 0; i < 4; ++i) {
+        const int64_t row = MODE == 0 || m0 + a_row[i] < M ? m0 + a_row[i] : M - 1;
+        ra[i] = *reinterpret_cast<const f64x2u*>(Ap + row * K + k0 + a_col0);
+      }
+#pragma unroll
+      for (int e = 0; e < 4; ++e) rb[e] = Bp[(k0 + 2 * b_p + e) * N + b_col];
     };
 
     auto store_slice = [&](int buf) {
@@ -594,24 +588,12 @@ __global__ __launch_bounds__(256) void zero_kernel(T* __restrict__ out, int64_t 
   for (int64_t i = int64_t(blockIdx.x) * 256 + threadIdx.x; i < count; i += int64_t(gridDim.x) * 256) out[i] = T(0);
 }
 
-template <typename T>
-bool aligned16(const T* p) {
-  return reinterpret_cast<uintptr_t>(p) % 16 == 0;
-}
-
 void prepare(int64_t m, int64_t n, int64_t batch, int64_t bm, int64_t bn, TileMap& tm) {
   tm.tiles_m = hp::ceil_div(m, bm);
   tm.tiles_n = hp::ceil_div(n, bn);
   tm.tiles_per_batch = tm.tiles_m * tm.tiles_n;
   tm.total = tm.tiles_per_batch * batch;
   hp::require(tm.total <= hp::kMaxGrid, "GEMM has too many tiles for one launch");
-}
-
-bool a_strides_aligned(const BatchDesc& bd, int64_t elems_per_16b) {
-  for (int d = 0; d < bd.rank; ++d) {
-    if (bd.a_stride[d] % elems_per_16b) return false;
-  }
-  return true;
 }
 
 // Workgroups of `kernel` resident per compute unit, queried once per kernel.
@@ -678,19 +660,15 @@ void run_f32(hp_ctx* ctx, const float* a, const float* b, float* c, int64_t m, i
   using namespace f32;
   TileMap tm;
   prepare(m, n, batch, BM, BN, tm);
-  const bool vec_ok = aligned16(a) && k % 4 == 0 && a_strides_aligned(bd, 4);
   auto fix = fixup_kernel<float, hpd::f32x4, Layout>;
-  if (vec_ok && k % BK == 0 && m % BM == 0 && n % BN == 0) {
+  if (k % BK == 0 && m % BM == 0 && n % BN == 0) {
     launch_split<float, BM, BN>(ctx, kernel<0, false>, kernel<0, true>, fix, kThreads, a, b, c, m, n, k, bd, tm, BK,
                                 "gemm_f32");
-  } else if (vec_ok && k % BK == 0) {
+  } else if (k % BK == 0) {
     launch_split<float, BM, BN>(ctx, kernel<1, false>, kernel<1, true>, fix, kThreads, a, b, c, m, n, k, bd, tm, BK,
                                 "gemm_f32");
-  } else if (vec_ok) {
-    launch_split<float, BM, BN>(ctx, kernel<2, false>, kernel<2, true>, fix, kThreads, a, b, c, m, n, k, bd, tm, BK,
-                                "gemm_f32");
   } else {
-    launch_split<float, BM, BN>(ctx, kernel<3, false>, kernel<3, true>, fix, kThreads, a, b, c, m, n, k, bd, tm, BK,
+    launch_split<float, BM, BN>(ctx, kernel<2, false>, kernel<2, true>, fix, kThreads, a, b, c, m, n, k, bd, tm, BK,
                                 "gemm_f32");
   }
 }
@@ -700,19 +678,15 @@ void run_f64(hp_ctx* ctx, const double* a, const double* b, double* c, int64_t m
   using namespace f64;
   TileMap tm;
   prepare(m, n, batch, BM, BN, tm);
-  const bool vec_ok = aligned16(a) && k % 2 == 0 && a_strides_aligned(bd, 2);
   auto fix = fixup_kernel<double, f64x4, Layout>;
-  if (vec_ok && k % BK == 0 && m % BM == 0 && n % BN == 0) {
+  if (k % BK == 0 && m % BM == 0 && n % BN == 0) {
     launch_split<double, BM, BN>(ctx, kernel<0, false>, kernel<0, true>, fix, kThreads, a, b, c, m, n, k, bd, tm, BK,
                                  "gemm_f64");
-  } else if (vec_ok && k % BK == 0) {
+  } else if (k % BK == 0) {
     launch_split<double, BM, BN>(ctx, kernel<1, false>, kernel<1, true>, fix, kThreads, a, b, c, m, n, k, bd, tm, BK,
                                  "gemm_f64");
-  } else if (vec_ok) {
-    launch_split<double, BM, BN>(ctx, kernel<2, false>, kernel<2, true>, fix, kThreads, a, b, c, m, n, k, bd, tm, BK,
-                                 "gemm_f64");
   } else {
-    launch_split<double, BM, BN>(ctx, kernel<3, false>, kernel<3, true>, fix, kThreads, a, b, c, m, n, k, bd, tm, BK,
+    launch_split<double, BM, BN>(ctx, kernel<2, false>, kernel<2, true>, fix, kThreads, a, b, c, m, n, k, bd, tm, BK,
                                  "gemm_f64");
   }
 }

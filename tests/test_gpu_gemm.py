@@ -9,6 +9,8 @@ oracle <= 2x the error of the reference kernel's sequential-K order
 (oracle.kernels.gemm_sequential) on the same sampled outputs.
 """
 
+import ctypes
+
 import numpy as np
 import pytest
 
@@ -107,10 +109,10 @@ def test_batched_broadcast_products(hip, dtype, shapes):
 @pytest.mark.parametrize(
     "m,n,k",
     [
-        (256, 128, 16),  # one interior tile
+        (256, 128, 16),  # one tile, M/N edge (clamped loads)
         (512, 256, 64),  # interior, several tiles and slices
-        (257, 129, 17),  # every edge guarded, scalar loads (K odd)
-        (300, 200, 100),  # guarded vector loads
+        (257, 129, 17),  # every edge, K odd (zero-filled K edge slice)
+        (300, 200, 100),  # K edge with K % 4 == 0
         (1, 1, 1),
         (31, 33, 4099),  # long K, partial tiles
         (640, 384, 48),
@@ -127,19 +129,19 @@ def test_kernel_modes_against_float64(hip, dtype, m, n, k):
     assert np.all(np.abs(got - want) <= bound * scale + 1e-30)
 
 
-# Tile counts that leave the last round of resident workgroups (256 compute
-# units x 2) partly filled, so their K slices are cut into stream-K runs and
-# summed by the fixup kernel: runs that cross tile boundaries (extra > 0),
+# Tile counts that leave the last round of resident workgroups (one per
+# compute unit) partly filled, so their K slices are cut into stream-K runs
+# and summed by the fixup kernel: runs that cross tile boundaries (extra > 0),
 # single-tile problems cut over many workers, batched tiles, every load mode.
 STREAM_K_CASES = [
-    (np.float32, (), 512, 256, 1552),  # interior, 4 tiles x 97 slices, runs of 9 and 8
+    (np.float32, (), 512, 256, 1552),  # interior, 2 tiles x 97 slices
     (np.float32, (), 31, 33, 4099),  # one tile cut over 32 workers
-    (np.float32, (), 1000, 700, 2000),  # guarded vector loads, 24 tiles
-    (np.float32, (), 777, 555, 1111),  # scalar loads (K odd)
-    (np.float32, (3,), 300, 200, 700),  # batched: 12 tiles
-    (np.float64, (), 1000, 1000, 2000),  # 64 tiles over 512 workers, extra > 0
+    (np.float32, (), 1000, 700, 2000),  # M/N edges, 12 tiles
+    (np.float32, (), 777, 555, 1111),  # K odd
+    (np.float32, (3,), 300, 200, 700),  # batched: 6 tiles
+    (np.float64, (), 1000, 1000, 2000),  # 32 tiles over 256 workers, extra > 0
     (np.float64, (2,), 256, 384, 1024),  # interior fp64, batched
-    (np.float64, (), 129, 65, 3001),  # scalar loads fp64
+    (np.float64, (), 129, 65, 3001),  # K odd, fp64
 ]
 
 
@@ -152,6 +154,32 @@ def test_stream_k_splits_against_float64_and_deterministic(hip, dtype, batch, m,
     got = p.asnumpy(A @ B)
     again = p.asnumpy(A @ B)
     np.testing.assert_array_equal(got, again)  # fixed K order: bitwise repeatable
+    want = a.astype(np.float64) @ b.astype(np.float64)
+    scale = np.abs(a).astype(np.float64) @ np.abs(b).astype(np.float64)
+    bound = (4e-7 if dtype == np.float32 else 8e-16) * np.sqrt(k) * 4
+    assert np.all(np.abs(got - want) <= bound * scale + 1e-30)
+
+
+@pytest.mark.parametrize("dtype", [np.float32, np.float64])
+@pytest.mark.parametrize("m,n,k", [(300, 260, 64), (512, 256, 48), (129, 70, 37)])
+def test_operands_at_element_alignment(hip, dtype, m, n, k):
+    """hp_gemm with A, B and C at an odd element offset (rows not 16-byte aligned)."""
+    rng = np.random.default_rng(m + n + k)
+    a = rng.uniform(-1, 1, (m, k)).astype(dtype)
+    b = rng.uniform(-1, 1, (k, n)).astype(dtype)
+    size = np.dtype(dtype).itemsize
+    pad = np.zeros(1, dtype)
+    A = hip.upload(np.concatenate([pad, a.ravel()]))
+    B = hip.upload(np.concatenate([pad, b.ravel()]))
+    C = hip.upload(np.full(m * n + 1, np.nan, dtype))
+    code = 5 if dtype == np.float32 else 6
+    with hip._active():
+        hip._call("hp_gemm", code, ctypes.c_void_p(A.ptr + size), ctypes.c_void_p(B.ptr + size),
+                  ctypes.c_void_p(C.ptr + size), m, n, k, 0, None, None, None)
+        out = np.empty(m * n + 1, dtype)
+        hip._call("hp_d2h", ctypes.c_void_p(out.ctypes.data), ctypes.c_void_p(C.ptr), out.nbytes)
+    assert np.isnan(out[0])  # the element before C is untouched
+    got = out[1:].reshape(m, n)
     want = a.astype(np.float64) @ b.astype(np.float64)
     scale = np.abs(a).astype(np.float64) @ np.abs(b).astype(np.float64)
     bound = (4e-7 if dtype == np.float32 else 8e-16) * np.sqrt(k) * 4
