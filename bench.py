@@ -242,7 +242,7 @@ def bench_extras(p, hip, only, skip_cpu):
         b = rng.uniform(-1, 1, (n, n), dtype="float64")
         ms, wall = timer.run(lambda: a @ b, 5)
         flops = 2.0 * n**3
-        extra["gemm_f64_4096"] = {"value": round(flops / (ms * 1e-3) / 1e9, 1), "unit": "GFLOP/s", "kernel_ms": round(ms, 4), "roofline": roofline("mfma_fp64", flops, ms)}
+        extra["gemm_f64_4096"] = {"value": round(flops / (ms * 1e-3) / 1e9, 1), "unit": "GFLOP/s", "kernel_ms": round(ms, 4), "roofline": roofline("mfma_fp64", flops, ms, _traffic("gemm_f64"))}
         del a, b
     if want("gemm_padded"):
         m, k, n = 4097, 3001, 2049
