@@ -159,6 +159,14 @@ int hp_gemm(hp_ctx* ctx, int dtype, const void* a, const void* b, void* c, int64
 int hp_gemv(hp_ctx* ctx, int dtype, const void* a, const void* x, void* y, int64_t rows,
             int64_t inner);
 
+/* y[r] = rhs[r] - (a @ x)[r]: the hp_gemv product of row r, rounded to the
+ * dtype, then one subtraction, in the same launch (the eager b - A @ x,
+ * bit for bit). inner == 0 copies rhs. y must not alias rhs or a.
+ * Replaces: _gemv.py:10-75 (residual_matvec_data), reached from
+ * _compiler.py:157-176 ("residual_matvec" plan steps). */
+int hp_gemv_residual(hp_ctx* ctx, int dtype, const void* a, const void* x, const void* rhs, void* y,
+                     int64_t rows, int64_t inner);
+
 /* out[0] = sum_i x[i] * y[i] (HP_F32/HP_F64); n == 0 writes 0.
  * Replaces: _cuda_gemv.py:47-95 with a 1-D left operand (DOT partials +
  * _cuda.py:449-491 reduce). */

@@ -8,7 +8,9 @@
 // Accumulation: per lane a fused multiply-add chain over its strided vectors,
 // then a 64-lane butterfly and a fixed-order sum of the four wave partials.
 // Reference semantics: _cuda_gemv.py:20-95 (rows flattened, one output per
-// row, zero-length rows give zeros).
+// row, zero-length rows give zeros). With `rhs` the kernels store the residual
+// rhs[r] - y[r] instead: the same product, rounded to T, then one subtraction
+// (the eager b - A @ x boundary of _gemv.py:10-75, fused).
 #include "common.h"
 
 namespace {
@@ -42,7 +44,8 @@ __device__ __forceinline__ T dot_vec(const V& a, const V& x, T acc) {
 
 // Sums `acc[r]` over the workgroup; lane r < kRows of wave 0 gets row r's total.
 template <typename T, int R>
-__device__ __forceinline__ void block_reduce_store(T (&acc)[R], T* y, int64_t r0, int64_t rows) {
+__device__ __forceinline__ void block_reduce_store(T (&acc)[R], T* y, int64_t r0, int64_t rows,
+                                                   const T* rhs = nullptr) {
   __shared__ T partial[kBlock / 64][R];
   const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
 #pragma unroll
@@ -55,13 +58,14 @@ __device__ __forceinline__ void block_reduce_store(T (&acc)[R], T* y, int64_t r0
     T total = partial[0][threadIdx.x];
 #pragma unroll
     for (int w = 1; w < kBlock / 64; ++w) total += partial[w][threadIdx.x];
-    y[r0 + threadIdx.x] = total;
+    y[r0 + threadIdx.x] = rhs ? rhs[r0 + threadIdx.x] - total : total;
   }
 }
 
 template <typename T>
 __global__ __launch_bounds__(kBlock) void gemv_vec_kernel(const T* __restrict__ a, const T* __restrict__ x,
-                                                          T* __restrict__ y, int64_t rows, int64_t inner) {
+                                                          const T* __restrict__ rhs, T* __restrict__ y, int64_t rows,
+                                                          int64_t inner) {
   using V = typename Vec<T>::type;
   const int64_t r0 = int64_t(blockIdx.x) * kRows;
   const int64_t nv = inner / Vec<T>::width;
@@ -93,13 +97,14 @@ __global__ __launch_bounds__(kBlock) void gemv_vec_kernel(const T* __restrict__ 
 #pragma unroll
     for (int r = 0; r < kRows; ++r) acc[r] = dot_vec(__builtin_nontemporal_load(av[r] + j), xs, acc[r]);
   }
-  block_reduce_store<T, kRows>(acc, y, r0, rows);
+  block_reduce_store<T, kRows>(acc, y, r0, rows, rhs);
 }
 
 // Scalar loads for rows whose length is not a multiple of the vector width.
 template <typename T>
 __global__ __launch_bounds__(kBlock) void gemv_scalar_kernel(const T* __restrict__ a, const T* __restrict__ x,
-                                                             T* __restrict__ y, int64_t rows, int64_t inner) {
+                                                             const T* __restrict__ rhs, T* __restrict__ y,
+                                                             int64_t rows, int64_t inner) {
   const int64_t r0 = int64_t(blockIdx.x) * kRows;
   const T* ar[kRows];
 #pragma unroll
@@ -110,13 +115,14 @@ __global__ __launch_bounds__(kBlock) void gemv_scalar_kernel(const T* __restrict
 #pragma unroll
     for (int r = 0; r < kRows; ++r) acc[r] = dfma(ar[r][j], xs, acc[r]);
   }
-  block_reduce_store<T, kRows>(acc, y, r0, rows);
+  block_reduce_store<T, kRows>(acc, y, r0, rows, rhs);
 }
 
 // Short rows: one wave per row, four rows per workgroup.
 template <typename T>
 __global__ __launch_bounds__(kBlock) void gemv_short_kernel(const T* __restrict__ a, const T* __restrict__ x,
-                                                            T* __restrict__ y, int64_t rows, int64_t inner) {
+                                                            const T* __restrict__ rhs, T* __restrict__ y,
+                                                            int64_t rows, int64_t inner) {
   const int lane = threadIdx.x & 63;
   const int64_t row = int64_t(blockIdx.x) * 4 + (threadIdx.x >> 6);
   if (row >= rows) return;
@@ -124,7 +130,7 @@ __global__ __launch_bounds__(kBlock) void gemv_short_kernel(const T* __restrict_
   T acc = T(0);
   for (int64_t j = lane; j < inner; j += 64) acc = dfma(ar[j], x[j], acc);
   acc = hpd::wave_sum(acc);
-  if (lane == 0) y[row] = acc;
+  if (lane == 0) y[row] = rhs ? rhs[row] - acc : acc;
 }
 
 // Dot product: each workgroup reduces one chunk; partials are summed by a
@@ -150,19 +156,19 @@ __global__ __launch_bounds__(kBlock) void sum_partials_kernel(const T* __restric
 }
 
 template <typename T>
-void run_gemv(hp_ctx* ctx, const T* a, const T* x, T* y, int64_t rows, int64_t inner) {
+void run_gemv(hp_ctx* ctx, const T* a, const T* x, const T* rhs, T* y, int64_t rows, int64_t inner) {
   const bool aligned = reinterpret_cast<uintptr_t>(a) % 16 == 0 && reinterpret_cast<uintptr_t>(x) % 16 == 0;
   if (inner < 1024) {
     const int64_t grid = hp::ceil_div(rows, 4);
     hp::require(grid <= hp::kMaxGrid, "too many rows for one launch");
-    gemv_short_kernel<T><<<grid, kBlock, 0, ctx->stream>>>(a, x, y, rows, inner);
+    gemv_short_kernel<T><<<grid, kBlock, 0, ctx->stream>>>(a, x, rhs, y, rows, inner);
   } else {
     const int64_t grid = hp::ceil_div(rows, kRows);
     hp::require(grid <= hp::kMaxGrid, "too many rows for one launch");
     if (aligned && inner % Vec<T>::width == 0) {
-      gemv_vec_kernel<T><<<grid, kBlock, 0, ctx->stream>>>(a, x, y, rows, inner);
+      gemv_vec_kernel<T><<<grid, kBlock, 0, ctx->stream>>>(a, x, rhs, y, rows, inner);
     } else {
-      gemv_scalar_kernel<T><<<grid, kBlock, 0, ctx->stream>>>(a, x, y, rows, inner);
+      gemv_scalar_kernel<T><<<grid, kBlock, 0, ctx->stream>>>(a, x, rhs, y, rows, inner);
     }
   }
   hp::check_launch("gemv");
@@ -192,23 +198,40 @@ using hp::require;
 
 extern "C" {
 
+// Shared by hp_gemv (rhs == nullptr) and hp_gemv_residual.
+static void gemv_entry(hp_ctx* ctx, int dtype, const void* a, const void* x, const void* rhs, void* y, int64_t rows,
+                       int64_t inner) {
+  hp::enter(ctx);
+  require(dtype == HP_F32 || dtype == HP_F64, "gemv supports float32 and float64");
+  require(rows >= 0 && inner >= 0, "negative extent");
+  if (rows == 0) return;
+  require(y != nullptr, "null output");
+  if (inner == 0 && rhs == nullptr) {
+    HP_CHECK(hipMemsetAsync(y, 0, size_t(rows) * hp::dtype_size(dtype), ctx->stream));
+    return;
+  }
+  if (inner == 0) {
+    // The product is empty: the residual is rhs itself, bit for bit.
+    HP_CHECK(hipMemcpyAsync(y, rhs, size_t(rows) * hp::dtype_size(dtype), hipMemcpyDeviceToDevice, ctx->stream));
+    return;
+  }
+  require(a != nullptr && x != nullptr, "null input");
+  if (dtype == HP_F32) {
+    run_gemv<float>(ctx, (const float*)a, (const float*)x, (const float*)rhs, (float*)y, rows, inner);
+  } else {
+    run_gemv<double>(ctx, (const double*)a, (const double*)x, (const double*)rhs, (double*)y, rows, inner);
+  }
+}
+
 int hp_gemv(hp_ctx* ctx, int dtype, const void* a, const void* x, void* y, int64_t rows, int64_t inner) {
+  return guarded([&] { gemv_entry(ctx, dtype, a, x, nullptr, y, rows, inner); });
+}
+
+int hp_gemv_residual(hp_ctx* ctx, int dtype, const void* a, const void* x, const void* rhs, void* y, int64_t rows,
+                     int64_t inner) {
   return guarded([&] {
-    hp::enter(ctx);
-    require(dtype == HP_F32 || dtype == HP_F64, "gemv supports float32 and float64");
-    require(rows >= 0 && inner >= 0, "negative extent");
-    if (rows == 0) return;
-    require(y != nullptr, "null output");
-    if (inner == 0) {
-      HP_CHECK(hipMemsetAsync(y, 0, size_t(rows) * hp::dtype_size(dtype), ctx->stream));
-      return;
-    }
-    require(a != nullptr && x != nullptr, "null input");
-    if (dtype == HP_F32) {
-      run_gemv<float>(ctx, (const float*)a, (const float*)x, (float*)y, rows, inner);
-    } else {
-      run_gemv<double>(ctx, (const double*)a, (const double*)x, (double*)y, rows, inner);
-    }
+    require(rows == 0 || rhs != nullptr, "null right-hand side");
+    gemv_entry(ctx, dtype, a, x, rhs, y, rows, inner);
   });
 }
 

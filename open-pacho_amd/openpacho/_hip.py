@@ -4,8 +4,8 @@ Protocol (reference backends.py:82-150 and _cuda.py:129-679): ``name``,
 ``device``, ``fp64``, ``validate_dtype``, ``empty``, ``full``, ``upload``,
 ``download``, ``elementwise``, ``gather``, ``reduce``, ``matmul``, ``norm``,
 ``synchronize``, ``random_distributions``, ``random_data``, plus the optional
-``create_lowering``, ``prepare_padded_matmul``, ``execution_scope``,
-``release_cached_memory`` and ``close``.
+``create_lowering``, ``prepare_padded_matmul``, ``residual_matvec``,
+``execution_scope``, ``release_cached_memory`` and ``close``.
 
 Storage is an _Allocation (device pointer + capacity) from the library's
 stream-ordered pool. All work of a backend runs on its single stream, so an
@@ -396,6 +396,12 @@ class HIPBackend:
         if len(dims) > 6:
             raise NotImplementedError("matmul supports at most 6 independent batch axes")
         return dims, ra, rb
+
+    def residual_matvec(self, a, x, b):
+        """``b - a @ x`` in one launch (plan step "residual_matvec")."""
+        from ._hip_gemv import residual_matvec_data
+
+        return residual_matvec_data(self, a, x, b)
 
     def prepare_padded_matmul(self, ashape, bshape, shape, dtype):
         from ._hip_padding import prepare

