@@ -154,6 +154,15 @@ int hp_gemm(hp_ctx* ctx, int dtype, const void* a, const void* b, void* c, int64
             int64_t k, int batch_rank, const int64_t* batch_shape, const int64_t* a_batch_strides,
             const int64_t* b_batch_strides);
 
+/* C = op(A) @ op(B), 2-D, m x n x k, row-major C. op(A) = A stored (m, k), or
+ * its transpose stored (k, m) when transpose_a; op(B) = B stored (k, n), or
+ * stored (n, k) when transpose_b. Same kernels, accumulation and K order as
+ * hp_gemm; k == 0 writes zeros; C is never read.
+ * Replaces: _matmul_layout.py:19-31 (TransposedGemm.run, a CLBlast GEMM with
+ * transpose flags), reached from _compiler.py:136-156 ("layout_matmul"). */
+int hp_gemm_layout(hp_ctx* ctx, int dtype, const void* a, const void* b, void* c, int64_t m, int64_t n,
+                   int64_t k, int transpose_a, int transpose_b);
+
 /* y[r] = sum_j a[r*inner + j] * x[j] for r < rows (HP_F32/HP_F64).
  * inner == 0 writes zeros. Replaces: _cuda_gemv.py:47-95 (matvec_data). */
 int hp_gemv(hp_ctx* ctx, int dtype, const void* a, const void* x, void* y, int64_t rows,

@@ -1,0 +1,33 @@
+// Shared declarations of the GEMM translation units (libpacho_hip.so
+// internals). The kernels are compiled once per dtype and operand layout in
+// gemm_<dtype>_<layout>.hip (n = stored as in the product, t = transposed)
+// so that the variants build in parallel; gemm.hip holds the entry points.
+#pragma once
+
+#include "common.h"
+
+namespace hpgemm {
+
+// Batch broadcast of a product: per batch axis its extent and the element
+// strides of A and B (0 = broadcast), C batches being contiguous.
+struct BatchDesc {
+  int rank;
+  int64_t shape[6];
+  int64_t a_stride[6];
+  int64_t b_stride[6];
+};
+
+// C[b] = op(A[b']) @ op(B[b'']) for b < batch, m x n x k, row-major; op(A)
+// is A stored [k][m] for layout t?, op(B) is B stored [n][k] for ?t.
+using Run = void (*)(hp_ctx* ctx, const void* a, const void* b, void* c, int64_t m, int64_t n, int64_t k,
+                     const BatchDesc& bd, int64_t batch);
+void f32_nn(hp_ctx*, const void*, const void*, void*, int64_t, int64_t, int64_t, const BatchDesc&, int64_t);
+void f32_tn(hp_ctx*, const void*, const void*, void*, int64_t, int64_t, int64_t, const BatchDesc&, int64_t);
+void f32_nt(hp_ctx*, const void*, const void*, void*, int64_t, int64_t, int64_t, const BatchDesc&, int64_t);
+void f32_tt(hp_ctx*, const void*, const void*, void*, int64_t, int64_t, int64_t, const BatchDesc&, int64_t);
+void f64_nn(hp_ctx*, const void*, const void*, void*, int64_t, int64_t, int64_t, const BatchDesc&, int64_t);
+void f64_tn(hp_ctx*, const void*, const void*, void*, int64_t, int64_t, int64_t, const BatchDesc&, int64_t);
+void f64_nt(hp_ctx*, const void*, const void*, void*, int64_t, int64_t, int64_t, const BatchDesc&, int64_t);
+void f64_tt(hp_ctx*, const void*, const void*, void*, int64_t, int64_t, int64_t, const BatchDesc&, int64_t);
+
+}  // namespace hpgemm

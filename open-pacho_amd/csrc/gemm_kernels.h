@@ -1,0 +1,731 @@
+// MFMA GEMM for gfx950: C[b] = A[b'] @ B[b''] in fp32 and fp64.
+//
+// fp32: v_mfma_f32_16x16x4_f32 (measured 155 TFLOP/s peak on MI355X, against
+// 137 for the 32x32x2 form). Workgroup tile 256x256x16, eight waves in a 2x4
+// grid, each wave 128x64 (8x4 MFMA blocks, 128 accumulators per lane); one
+// workgroup per compute unit. Against a 256x128 tile at two workgroups per CU
+// this halves the global/L2 -> LDS traffic per flop (measured +4% of peak).
+// fp64: v_mfma_f64_16x16x4_f64, workgroup tile 256x128x16, eight waves in a
+// 4x2 grid of 64x64 wave tiles, one workgroup per compute unit.
+//
+// Data path per K slice: global -> registers (prefetched ahead) -> LDS
+// (double-buffered, one barrier per slice) -> 16-byte LDS reads -> MFMA. LDS
+// holds both operands k-contiguous: A as [m][k] (a copy of a row-major tile)
+// and B as [n][k] (each lane loads one column's k values as scalars, so the
+// transposition costs no shuffles). A lane of MFMA lane group g = lane/16
+// then reads four consecutive k values with one ds_read_b128 and feeds them to
+// four MFMAs, i.e. MFMA number q contracts k = {q, 4+q, 8+q, 12+q}; A and B
+// use the same permutation, so every product of the slice is summed exactly
+// once.
+//
+// Schedule. Tiles are numbered batch-major and, inside a batch, in groups of
+// kGroupM tile rows, so neighbouring tiles share A and B panels. Whole rounds
+// of resident workgroups (compute units x workgroups per CU) each take one
+// tile and its full K range; workgroup ids are renumbered so each XCD (ids
+// i % 8) owns a contiguous range of tiles and its L2 sees shared panels. The
+// tiles of a last, partly filled round are instead cut into equal runs of K
+// slices over every resident slot (stream-K): a worker's run covers the end
+// of one tile and the start of the next, and every cut piece goes to a
+// workspace. A second kernel adds the pieces of each cut tile in K order, so
+// results are deterministic. Without this, e.g. 153 tiles on 256 compute units
+// leave 103 of them idle for the whole product.
+//
+// Modes: 0 = interior (no guards; M, N, K multiples of the tile), 1 = M/N
+// edges (K a multiple of 16): edge rows and columns load clamped addresses
+// and only the stores are masked, since they feed no stored output; 2 = any
+// K: as 1, plus the one slice holding the K edge takes scalar loads that
+// zero-fill past K, so it contracts against +0 padding. A rows are read as
+// 16-byte vectors at element alignment (odd K included).
+//
+// Reference semantics: _gemm.py:24-137 (per-batch broadcast offsets
+// _offset :13-21, never reads C), _cuda.py:493-518 and :619-636.
+// (Device code and host launch templates; included by the gemm_<dtype>_<layout>
+// translation units only.)
+#pragma once
+
+#include <algorithm>
+
+#include "gemm.h"
+
+namespace {
+
+using hpgemm::BatchDesc;
+
+struct TileMap {
+  int64_t tiles_m, tiles_n, tiles_per_batch, total;
+};
+
+// Division of the tile space between whole-tile workgroups and stream-K
+// workers. Logical tiles [0, dp_tiles) run whole; the K slices of tiles
+// [dp_tiles, total) are dealt out in consecutive runs, worker w owning
+// base + (w < extra) slices starting at sk_begin(w).
+struct Split {
+  int64_t dp_tiles;
+  int64_t workers;
+  int64_t base, extra;
+  int64_t slices;  // K slices per tile
+  void* partial;   // [workers][2][tile elements]: a worker's first and last cut piece
+};
+
+constexpr int64_t kGroupM = 8;
+
+// 16-byte operand loads that need only element alignment (rows of an odd K
+// or a view at any element offset): one global_load_dwordx4 all the same.
+typedef float f32x4u __attribute__((ext_vector_type(4), aligned(4)));
+typedef double f64x2u __attribute__((ext_vector_type(2), aligned(8)));
+constexpr int64_t kMinSlices = 8;  // shortest stream-K run
+
+__device__ __forceinline__ void logical_tile(int64_t t, const TileMap& tm, int64_t& batch, int64_t& ti,
+                                             int64_t& tj) {
+  batch = t / tm.tiles_per_batch;
+  t -= batch * tm.tiles_per_batch;
+  const int64_t group = t / (kGroupM * tm.tiles_n);
+  const int64_t first = group * kGroupM;
+  const int64_t gm = tm.tiles_m - first < kGroupM ? tm.tiles_m - first : kGroupM;
+  const int64_t r = t - group * kGroupM * tm.tiles_n;
+  ti = first + r % gm;
+  tj = r / gm;
+}
+
+// Consecutive ids of a count-long range, renumbered so that ids landing on one
+// XCD (ids i % 8) get a contiguous block of the range.
+__device__ __forceinline__ int64_t xcd_major(int64_t id, int64_t count) {
+  const int64_t full = (count / 8) * 8;
+  return id < full ? (id % 8) * (full / 8) + id / 8 : id;
+}
+
+__host__ __device__ __forceinline__ int64_t sk_begin(const Split& sp, int64_t w) {
+  return w * sp.base + (w < sp.extra ? w : sp.extra);
+}
+
+__device__ __forceinline__ int64_t sk_worker(const Split& sp, int64_t g) {
+  const int64_t long_runs = sp.extra * (sp.base + 1);
+  return g < long_runs ? g / (sp.base + 1) : sp.extra + (g - long_runs) / sp.base;
+}
+
+__device__ __forceinline__ void batch_offsets(int64_t batch, const BatchDesc& bd, int64_t& a_off, int64_t& b_off) {
+  a_off = 0;
+  b_off = 0;
+  int64_t rest = batch;
+  for (int d = bd.rank - 1; d >= 0; --d) {
+    const int64_t extent = bd.shape[d];
+    const int64_t q = rest / extent;
+    const int64_t idx = rest - q * extent;
+    rest = q;
+    a_off += idx * bd.a_stride[d];
+    b_off += idx * bd.b_stride[d];
+  }
+}
+
+// ---------------------------------------------------------------- loaders ----
+
+template <typename T>
+struct Vec16;
+template <>
+struct Vec16<float> {
+  using type = hpd::f32x4;
+  using loose = f32x4u;
+};
+template <>
+struct Vec16<double> {
+  using type = hpd::f64x2;
+  using loose = f64x2u;
+};
+
+// One operand's K slice: ROWS tile rows x 16 k values, global -> registers
+// -> LDS rows [row][16 k] in 16-byte groups, group g of row r stored at slot
+// g ^ ((r >> 1) & (G - 1)) (G groups per row; conflict-free fragment reads,
+// see the kernels).
+//   KM = false: stored k-contiguous, element (r, k) at p[r * ld + k] (A, or
+//     B transposed). Each thread loads whole 16-byte groups.
+//   KM = true: stored row-contiguous, element (r, k) at p[k * ld + r] (B, or
+//     A transposed). Each thread owns one row and loads NE consecutive k as
+//     scalars; 64 lanes read 64 consecutive rows of one k.
+// Rows past `rows` load clamped addresses (their outputs are never stored);
+// in mode 2 the slice holding the K edge zero-fills past kp.
+template <typename T, int ROWS, bool KM, int MODE, int THREADS>
+struct SliceLoader {
+  using V = typename Vec16<T>::type;
+  using VL = typename Vec16<T>::loose;
+  static constexpr int W = 16 / sizeof(T);         // elements per group
+  static constexpr int G = 16 / W;                 // groups per LDS row
+  static constexpr int NV = ROWS * G / THREADS;    // groups per thread (KM = false)
+  static constexpr int NE = 16 * ROWS / THREADS;   // elements per thread (KM = true)
+  static constexpr int NR = KM ? NE / W : NV;      // register groups per thread
+  static_assert(NV >= 1 && NE % W == 0, "tile does not divide over the workgroup");
+
+  V reg[NR];
+  int lds[NR];  // LDS element offsets of the register groups
+  int row0;     // KM = false: first row of this thread; true: its row
+  int kbase;    // KM = true: first k of this thread in the slice
+
+  __device__ __forceinline__ static int swz(int row) { return (row >> 1) & (G - 1); }
+
+  __device__ __forceinline__ void init(int tid) {
+    if (!KM) {
+      const int g = tid % G;
+      row0 = tid / G;
+      kbase = g * W;
+#pragma unroll
+      for (int i = 0; i < NV; ++i) {
+        const int r = row0 + (THREADS / G) * i;
+        lds[i] = r * 16 + W * (g ^ swz(r));
+      }
+    } else {
+      row0 = tid % ROWS;
+      kbase = (tid / ROWS) * NE;
+#pragma unroll
+      for (int j = 0; j < NR; ++j) lds[j] = row0 * 16 + W * ((kbase / W + j) ^ swz(row0));
+    }
+  }
+
+  // p: operand origin at this piece's first k; r0: first tile row; rows:
+  // operand rows; ld: leading dimension; kp: valid k from the origin.
+  __device__ __forceinline__ void load(const T* p, int64_t r0, int64_t rows, int64_t ld, int64_t kp, int64_t k0) {
+    if (!KM) {
+      if (MODE == 2 && k0 + 16 > kp) {
+#pragma unroll
+        for (int i = 0; i < NV; ++i) {
+          const int64_t r = r0 + row0 + (THREADS / G) * i;
+          const T* q = p + (r < rows ? r : rows - 1) * ld;
+#pragma unroll
+          for (int e = 0; e < W; ++e) reg[i][e] = k0 + kbase + e < kp ? q[k0 + kbase + e] : T(0);
+        }
+        return;
+      }
+#pragma unroll
+      for (int i = 0; i < NV; ++i) {
+        const int64_t r = r0 + row0 + (THREADS / G) * i;
+        reg[i] = *reinterpret_cast<const VL*>(p + (MODE == 0 || r < rows ? r : rows - 1) * ld + k0 + kbase);
+      }
+    } else {
+      const int64_t r = MODE == 0 || r0 + row0 < rows ? r0 + row0 : rows - 1;
+      if (MODE == 2 && k0 + 16 > kp) {
+#pragma unroll
+        for (int e = 0; e < NE; ++e) {
+          const int64_t k = k0 + kbase + e;
+          reg[e / W][e % W] = k < kp ? p[k * ld + r] : T(0);
+        }
+        return;
+      }
+#pragma unroll
+      for (int e = 0; e < NE; ++e) reg[e / W][e % W] = p[(k0 + kbase + e) * ld + r];
+    }
+  }
+
+  __device__ __forceinline__ void store(T* buf) const {
+#pragma unroll
+    for (int j = 0; j < NR; ++j) *reinterpret_cast<V*>(buf + lds[j]) = reg[j];
+  }
+
+  // Element offset of the operand origin for a piece starting at slice s0.
+  __device__ __forceinline__ static int64_t origin(int64_t s0, int64_t ld) { return KM ? s0 * 16 * ld : s0 * 16; }
+};
+
+// ------------------------------------------------------------------ fp32 ----
+
+namespace f32 {
+
+constexpr int BM = 256, BN = 256, BK = 16;
+constexpr int S = BK;  // LDS row stride (floats): 16-float rows, swizzled quads
+constexpr int kThreads = 512;
+constexpr int FM = 8, FN = 4;  // MFMA blocks per wave
+constexpr int WM = 128, WN = 64;
+
+// LDS rows hold 4 quads of 4 consecutive k values; quad q of row r is stored
+// at slot q ^ ((r >> 1) & 3). Rows are 16 floats (64 B), so a ds_read_b128 by
+// lanes reading rows r0..r0+15 at one logical quad, a ds_write_b128 of 4 rows x
+// 4 quads, and the B writes of 16 consecutive n at one quad all land on
+// distinct banks (measured: removes the LDS bank conflicts of padded rows).
+__device__ __forceinline__ int swizzle(int row) { return (row >> 1) & 3; }
+
+// Eight waves in a 2x4 grid of 128x64 wave tiles. Accumulator layout: lane
+// holds column lane%16, rows 4*(lane/16) + r.
+struct Layout {
+  static constexpr int kBM = BM, kBN = BN, kFM = FM, kFN = FN;
+  static __device__ __forceinline__ int row(int wave, int i, int lane, int r) {
+    return (wave >> 2) * WM + 16 * i + 4 * (lane >> 4) + r;
+  }
+  static __device__ __forceinline__ int col(int wave, int j, int lane) { return (wave & 3) * WN + 16 * j + (lane & 15); }
+};
+
+// One workgroup per compute unit (64 KB of LDS, 2 waves per SIMD). The
+// pipeline per K slice s:
+//   - global loads of slice s+2 into registers, issued first;
+//   - 128 MFMAs per wave on the fragments of slice s, already in registers;
+//     after the 16 MFMAs of A fragment i, that register is refilled with
+//     fragment i of slice s+1 from LDS (B fragments are double-buffered), so
+//     LDS reads overlap the matrix pipe instead of stalling each slice start;
+//   - after the MFMAs of fragment 5, slice s+2 goes from registers to the LDS
+//     buffer that held slice s (all waves read it during slice s-1);
+//   - one barrier.
+// STREAM_K = false: workgroup b computes whole tile xcd_major(b). true:
+// workgroup b is stream-K worker xcd_major(b) and computes its run, at most
+// the end of one tile and the start of the next (kept out of the whole-tile
+// kernel: the second inlined piece measurably slows the main loop).
+template <int MODE, bool STREAM_K, bool TA, bool TB>
+__global__ __launch_bounds__(kThreads, 1) void kernel(const float* __restrict__ A, const float* __restrict__ B,
+                                                      float* __restrict__ C, int64_t M, int64_t N, int64_t K,
+                                                      BatchDesc bd, TileMap tmap, Split sp) {
+  __shared__ __attribute__((aligned(16))) float As[2][BM * S];
+  __shared__ __attribute__((aligned(16))) float Bs[2][BN * S];
+
+  const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
+  const int wm = wave >> 2, wn = wave & 3;
+
+  // Global -> register -> LDS operand slices. A is k-contiguous ([m][k])
+  // unless TA ([k][m]); B is row-contiguous ([k][n]) unless TB ([n][k]).
+  // Untransposed: A as 2 float4 per thread (rows tid/4 + 128i, k quad
+  // tid%4), B as 8 scalars per thread (column tid%256, k quads
+  // 2*(tid/256) + {0, 1}; 64 lanes read 256 contiguous bytes of one B row).
+  SliceLoader<float, BM, TA, MODE, kThreads> la;
+  SliceLoader<float, BN, !TB, MODE, kThreads> lb;
+  la.init(tid);
+  lb.init(tid);
+  const int64_t lda = TA ? M : K, ldb = TB ? K : N;
+  // Rows read by a lane differ by multiples of 16, so the swizzle of every
+  // row it reads equals that of (lane & 15).
+  const int a_read = (wm * WM + (lane & 15)) * S + 4 * ((lane >> 4) ^ swizzle(lane & 15));
+  const int b_read = (wn * WN + (lane & 15)) * S + 4 * ((lane >> 4) ^ swizzle(lane & 15));
+
+  // Tile `tile` over K slices [s0, s1). slot < 0: the piece is the whole K
+  // range and is stored to C; else it goes to workspace slot `slot`.
+  auto piece = [&](int64_t tile, int64_t s0, int64_t s1, int64_t slot) {
+    int64_t batch, ti, tj;
+    logical_tile(tile, tmap, batch, ti, tj);
+    int64_t a_off, b_off;
+    batch_offsets(batch, bd, a_off, b_off);
+    const int64_t m0 = ti * BM, n0 = tj * BN;
+    // Operand origins at the piece's first k; kp = valid k extent from there.
+    const float* Ap = A + a_off + decltype(la)::origin(s0, lda);
+    const float* Bp = B + b_off + decltype(lb)::origin(s0, ldb);
+    const int64_t kp = K - s0 * BK;
+    const int64_t slices = s1 - s0;
+    auto load_slice = [&](int64_t k0) {
+      la.load(Ap, m0, M, lda, kp, k0);
+      lb.load(Bp, n0, N, ldb, kp, k0);
+    };
+    auto store_slice = [&](int buf) {
+      la.store(As[buf]);
+      lb.store(Bs[buf]);
+    };
+
+    hpd::f32x4 acc[FM][FN];
+#pragma unroll
+    for (int i = 0; i < FM; ++i)
+#pragma unroll
+      for (int j = 0; j < FN; ++j) acc[i][j] = hpd::f32x4{0.f, 0.f, 0.f, 0.f};
+
+    load_slice(0);
+    store_slice(0);
+    if (slices > 1) {
+      load_slice(BK);
+      store_slice(1);
+    }
+    __syncthreads();
+    hpd::f32x4 a[FM], b[FN], b_next[FN];
+#pragma unroll
+    for (int i = 0; i < FM; ++i) a[i] = *reinterpret_cast<const hpd::f32x4*>(&As[0][a_read + 16 * i * S]);
+#pragma unroll
+    for (int j = 0; j < FN; ++j) b[j] = *reinterpret_cast<const hpd::f32x4*>(&Bs[0][b_read + 16 * j * S]);
+    __syncthreads();  // every wave has read buffer 0 before slice 0 refills it
+    // Fragment read addresses of the next slice, carried across iterations:
+    // indexing As[(s + 1) & 1] directly lets the compiler rematerialize the
+    // address into each fragment register, and that write has to wait for
+    // the MFMAs still reading the register (measured: -3% of peak).
+    const float* a_src = &As[1][a_read];
+    const float* b_src = &Bs[1][b_read];
+    for (int64_t s = 0; s < slices; ++s) {
+      const bool more = s + 1 < slices;
+      if (s + 2 < slices) load_slice((s + 2) * BK);
+#pragma unroll
+      for (int i = 0; i < FM; ++i) {
+#pragma unroll
+        for (int q = 0; q < 4; ++q)
+#pragma unroll
+          for (int j = 0; j < FN; ++j)
+            acc[i][j] = __builtin_amdgcn_mfma_f32_16x16x4f32(a[i][q], b[j][q], acc[i][j], 0, 0, 0);
+        if (more) {
+          a[i] = *reinterpret_cast<const hpd::f32x4*>(a_src + 16 * i * S);
+          if (i >= FM - FN) b_next[i - (FM - FN)] = *reinterpret_cast<const hpd::f32x4*>(b_src + 16 * (i - (FM - FN)) * S);
+        }
+        if (i == 5 && s + 2 < slices) store_slice(int(s & 1));
+      }
+#pragma unroll
+      for (int j = 0; j < FN; ++j) b[j] = b_next[j];
+      a_src = (s & 1) ? &As[1][a_read] : &As[0][a_read];
+      b_src = (s & 1) ? &Bs[1][b_read] : &Bs[0][b_read];
+      __syncthreads();
+    }
+
+    if (slot < 0) {
+      float* Cb = C + batch * M * N;
+#pragma unroll
+      for (int i = 0; i < FM; ++i) {
+#pragma unroll
+        for (int j = 0; j < FN; ++j) {
+          const int64_t col = n0 + Layout::col(wave, j, lane);
+#pragma unroll
+          for (int r = 0; r < 4; ++r) {
+            const int64_t row = m0 + Layout::row(wave, i, lane, r);
+            if (MODE == 0 || (row < M && col < N)) Cb[row * N + col] = acc[i][j][r];
+          }
+        }
+      }
+    } else {
+      // Cut piece: whole accumulator tile to the workspace slot, in register
+      // order (16 contiguous bytes per lane).
+      hpd::f32x4* out = static_cast<hpd::f32x4*>(sp.partial) + slot * (BM * BN / 4);
+#pragma unroll
+      for (int i = 0; i < FM; ++i)
+#pragma unroll
+        for (int j = 0; j < FN; ++j) out[((wave * FM + i) * FN + j) * 64 + lane] = acc[i][j];
+    }
+  };
+
+  if (!STREAM_K) {
+    piece(xcd_major(blockIdx.x, sp.dp_tiles), 0, sp.slices, -1);
+  } else {
+    const int64_t worker = xcd_major(blockIdx.x, sp.workers);
+    const int64_t g = sk_begin(sp, worker), g_end = sk_begin(sp, worker + 1);
+    // A run is at most one tile long: the end of one tile and the start of
+    // the next at most.
+    const int64_t t0 = g / sp.slices;
+    const int64_t s0 = g - t0 * sp.slices;
+    const int64_t s1 = g_end - t0 * sp.slices < sp.slices ? g_end - t0 * sp.slices : sp.slices;
+    piece(sp.dp_tiles + t0, s0, s1, s0 == 0 && s1 == sp.slices ? -1 : worker * 2);
+    const int64_t rest = g_end - (t0 + 1) * sp.slices;
+    if (rest > 0) piece(sp.dp_tiles + t0 + 1, 0, rest, rest == sp.slices ? -1 : worker * 2 + 1);
+  }
+}
+
+}  // namespace f32
+
+// ------------------------------------------------------------------ fp64 ----
+
+namespace f64 {
+
+constexpr int BM = 256, BN = 128, BK = 16;
+constexpr int S = BK;  // LDS row stride (doubles): 8 swizzled k pairs of 16 bytes
+constexpr int kThreads = 512;
+constexpr int FM = 4, FN = 4;
+constexpr int WM = 64, WN = 64;
+
+typedef double f64x4 __attribute__((ext_vector_type(4)));
+
+// LDS rows hold 8 pairs of consecutive k values; pair p of row r is stored at
+// slot p ^ ((r >> 1) & 7). Rows are 128 bytes, so 16 lanes reading one pair of
+// rows r0..r0+15 (fragment reads), writing 8 pairs of 2 rows (A stores) or one
+// pair of 16 rows (B stores) touch 16 distinct 16-byte bank groups.
+__device__ __forceinline__ int swizzle(int row) { return (row >> 1) & 7; }
+
+// Eight waves in a 4x2 grid of 64x64 wave tiles. f64 accumulator layout: lane
+// holds column lane%16, rows 4*r + lane/16.
+struct Layout {
+  static constexpr int kBM = BM, kBN = BN, kFM = FM, kFN = FN;
+  static __device__ __forceinline__ int row(int wave, int i, int lane, int r) {
+    return (wave >> 1) * WM + 16 * i + 4 * r + (lane >> 4);
+  }
+  static __device__ __forceinline__ int col(int wave, int j, int lane) { return (wave & 1) * WN + 16 * j + (lane & 15); }
+};
+
+// One workgroup per compute unit, the pipeline of the fp32 kernel: per slice,
+// global loads of slice s+2 first; MFMAs of slice s in two k halves of 8,
+// each A fragment refilled from LDS with slice s+1 right after its MFMAs and
+// the B fragments of a half after that half; slice s+2 to LDS after half 0;
+// one barrier. A lane of MFMA lane group g = lane/16 reads the k pair
+// {2g, 2g+1} (half 0) or {8+2g, 9+2g} (half 1) with one ds_read_b128 and
+// feeds it to two MFMAs (k-permutation shared by A and B).
+template <int MODE, bool STREAM_K, bool TA, bool TB>
+__global__ __launch_bounds__(kThreads, 1) void kernel(const double* __restrict__ A, const double* __restrict__ B,
+                                                      double* __restrict__ C, int64_t M, int64_t N, int64_t K,
+                                                      BatchDesc bd, TileMap tmap, Split sp) {
+  __shared__ __attribute__((aligned(16))) double As[2][BM * S];
+  __shared__ __attribute__((aligned(16))) double Bs[2][BN * S];
+
+  const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
+  const int wm = wave >> 1, wn = wave & 1;
+
+  // Operand slices as in the fp32 kernel. Untransposed: A as 4 double2 per
+  // thread (rows tid/8 + 64i, k pair tid%8), B as 4 scalars per thread
+  // (column tid%128, k rows 4*(tid/128) + {0..3}; 64 lanes read 512
+  // contiguous bytes of one B row), stored as 2 pairs.
+  SliceLoader<double, BM, TA, MODE, kThreads> la;
+  SliceLoader<double, BN, !TB, MODE, kThreads> lb;
+  la.init(tid);
+  lb.init(tid);
+  const int64_t lda = TA ? M : K, ldb = TB ? K : N;
+  // Fragment rows differ from (lane & 15) by multiples of 16: same swizzle.
+  const int sw = swizzle(lane & 15), g = lane >> 4;
+  const int a_read0 = (wm * WM + (lane & 15)) * S + 2 * (g ^ sw);
+  const int a_read1 = (wm * WM + (lane & 15)) * S + 2 * ((4 + g) ^ sw);
+  const int b_read0 = (wn * WN + (lane & 15)) * S + 2 * (g ^ sw);
+  const int b_read1 = (wn * WN + (lane & 15)) * S + 2 * ((4 + g) ^ sw);
+
+  auto piece = [&](int64_t tile, int64_t s0, int64_t s1, int64_t slot) {
+    int64_t batch, ti, tj;
+    logical_tile(tile, tmap, batch, ti, tj);
+    int64_t a_off, b_off;
+    batch_offsets(batch, bd, a_off, b_off);
+    const int64_t m0 = ti * BM, n0 = tj * BN;
+    const double* Ap = A + a_off + decltype(la)::origin(s0, lda);
+    const double* Bp = B + b_off + decltype(lb)::origin(s0, ldb);
+    const int64_t kp = K - s0 * BK;
+    const int64_t slices = s1 - s0;
+    auto load_slice = [&](int64_t k0) {
+      la.load(Ap, m0, M, lda, kp, k0);
+      lb.load(Bp, n0, N, ldb, kp, k0);
+    };
+    auto store_slice = [&](int buf) {
+      la.store(As[buf]);
+      lb.store(Bs[buf]);
+    };
+
+    f64x4 acc[FM][FN];
+#pragma unroll
+    for (int i = 0; i < FM; ++i)
+#pragma unroll
+      for (int j = 0; j < FN; ++j) acc[i][j] = f64x4{0.0, 0.0, 0.0, 0.0};
+
+    load_slice(0);
+    store_slice(0);
+    if (slices > 1) {
+      load_slice(BK);
+      store_slice(1);
+    }
+    __syncthreads();
+    hpd::f64x2 a[2][FM], b[2][FN];
+#pragma unroll
+    for (int i = 0; i < FM; ++i) {
+      a[0][i] = *reinterpret_cast<const hpd::f64x2*>(&As[0][a_read0 + 16 * i * S]);
+      a[1][i] = *reinterpret_cast<const hpd::f64x2*>(&As[0][a_read1 + 16 * i * S]);
+    }
+#pragma unroll
+    for (int j = 0; j < FN; ++j) {
+      b[0][j] = *reinterpret_cast<const hpd::f64x2*>(&Bs[0][b_read0 + 16 * j * S]);
+      b[1][j] = *reinterpret_cast<const hpd::f64x2*>(&Bs[0][b_read1 + 16 * j * S]);
+    }
+    __syncthreads();  // every wave has read buffer 0 before slice 0 refills it
+    // Next-slice LDS buffers, carried across iterations (see the fp32 kernel).
+    const double* a_src = As[1];
+    const double* b_src = Bs[1];
+    for (int64_t s = 0; s < slices; ++s) {
+      const bool more = s + 1 < slices;
+      if (s + 2 < slices) load_slice((s + 2) * BK);
+#pragma unroll
+      for (int h = 0; h < 2; ++h) {
+        const int a_read = h == 0 ? a_read0 : a_read1;
+        const int b_read = h == 0 ? b_read0 : b_read1;
+#pragma unroll
+        for (int i = 0; i < FM; ++i) {
+#pragma unroll
+          for (int q = 0; q < 2; ++q)
+#pragma unroll
+            for (int j = 0; j < FN; ++j)
+              acc[i][j] = __builtin_amdgcn_mfma_f64_16x16x4f64(a[h][i][q], b[h][j][q], acc[i][j], 0, 0, 0);
+          if (more) a[h][i] = *reinterpret_cast<const hpd::f64x2*>(a_src + a_read + 16 * i * S);
+        }
+        if (more) {
+#pragma unroll
+          for (int j = 0; j < FN; ++j) b[h][j] = *reinterpret_cast<const hpd::f64x2*>(b_src + b_read + 16 * j * S);
+        }
+        if (h == 0 && s + 2 < slices) store_slice(int(s & 1));
+      }
+      a_src = (s & 1) ? As[1] : As[0];
+      b_src = (s & 1) ? Bs[1] : Bs[0];
+      __syncthreads();
+    }
+
+    if (slot < 0) {
+      double* Cb = C + batch * M * N;
+#pragma unroll
+      for (int i = 0; i < FM; ++i) {
+#pragma unroll
+        for (int j = 0; j < FN; ++j) {
+          const int64_t col = n0 + Layout::col(wave, j, lane);
+#pragma unroll
+          for (int r = 0; r < 4; ++r) {
+            const int64_t row = m0 + Layout::row(wave, i, lane, r);
+            if (MODE == 0 || (row < M && col < N)) Cb[row * N + col] = acc[i][j][r];
+          }
+        }
+      }
+    } else {
+      f64x4* out = static_cast<f64x4*>(sp.partial) + slot * (BM * BN / 4);
+#pragma unroll
+      for (int i = 0; i < FM; ++i)
+#pragma unroll
+        for (int j = 0; j < FN; ++j) out[((wave * FM + i) * FN + j) * 64 + lane] = acc[i][j];
+    }
+  };
+
+  if (!STREAM_K) {
+    piece(xcd_major(blockIdx.x, sp.dp_tiles), 0, sp.slices, -1);
+  } else {
+    const int64_t worker = xcd_major(blockIdx.x, sp.workers);
+    const int64_t g0 = sk_begin(sp, worker), g_end = sk_begin(sp, worker + 1);
+    const int64_t t0 = g0 / sp.slices;
+    const int64_t s0 = g0 - t0 * sp.slices;
+    const int64_t s1 = g_end - t0 * sp.slices < sp.slices ? g_end - t0 * sp.slices : sp.slices;
+    piece(sp.dp_tiles + t0, s0, s1, s0 == 0 && s1 == sp.slices ? -1 : worker * 2);
+    const int64_t rest = g_end - (t0 + 1) * sp.slices;
+    if (rest > 0) piece(sp.dp_tiles + t0 + 1, 0, rest, rest == sp.slices ? -1 : worker * 2 + 1);
+  }
+}
+
+}  // namespace f64
+
+// Adds the cut pieces of each stream-K tile in K order (workers in increasing
+// order own increasing K ranges) and stores the tile. Tiles that one worker
+// covered whole were stored by it. One thread per accumulator 4-vector.
+template <typename T, typename V, typename L>
+__global__ __launch_bounds__(256) void fixup_kernel(T* __restrict__ C, int64_t M, int64_t N, TileMap tmap,
+                                                    Split sp) {
+  constexpr int BM = L::kBM, BN = L::kBN, FM = L::kFM, FN = L::kFN;
+  constexpr int kVectors = BM * BN / 4;
+  constexpr int kBlocksPerTile = kVectors / 256;
+  const int64_t tl = blockIdx.x / kBlocksPerTile;
+  const int v = (blockIdx.x % kBlocksPerTile) * 256 + threadIdx.x;
+  const int64_t g0 = tl * sp.slices;
+  const int64_t w0 = sk_worker(sp, g0), w1 = sk_worker(sp, g0 + sp.slices - 1);
+  if (w0 == w1) return;
+  const V* partial = static_cast<const V*>(sp.partial);
+  // w0 holds the tile's K start: as its first piece when its run starts
+  // there, else as its last. Later workers start inside the tile.
+  V sum = partial[(w0 * 2 + (sk_begin(sp, w0) == g0 ? 0 : 1)) * kVectors + v];
+  for (int64_t w = w0 + 1; w <= w1; ++w) sum = sum + partial[w * 2 * kVectors + v];
+  const int lane = v & 63;
+  const int block = v >> 6;
+  const int wave = block / (FM * FN);
+  const int i = (block / FN) % FM;
+  const int j = block % FN;
+  int64_t batch, ti, tj;
+  logical_tile(sp.dp_tiles + tl, tmap, batch, ti, tj);
+  T* Cb = C + batch * M * N;
+  const int64_t col = tj * BN + L::col(wave, j, lane);
+#pragma unroll
+  for (int r = 0; r < 4; ++r) {
+    const int64_t row = ti * BM + L::row(wave, i, lane, r);
+    if (row < M && col < N) Cb[row * N + col] = sum[r];
+  }
+}
+
+
+void prepare(int64_t m, int64_t n, int64_t batch, int64_t bm, int64_t bn, TileMap& tm) {
+  tm.tiles_m = hp::ceil_div(m, bm);
+  tm.tiles_n = hp::ceil_div(n, bn);
+  tm.tiles_per_batch = tm.tiles_m * tm.tiles_n;
+  tm.total = tm.tiles_per_batch * batch;
+  hp::require(tm.total <= hp::kMaxGrid, "GEMM has too many tiles for one launch");
+}
+
+// Workgroups of `kernel` resident per compute unit, queried once per kernel.
+template <typename F>
+int resident_per_cu(F kernel, int threads) {
+  static std::mutex mutex;
+  static std::unordered_map<const void*, int> known;
+  const void* key = reinterpret_cast<const void*>(kernel);
+  std::lock_guard<std::mutex> lock(mutex);
+  auto it = known.find(key);
+  if (it != known.end()) return it->second;
+  int blocks = 0;
+  HP_CHECK(hipOccupancyMaxActiveBlocksPerMultiprocessor(&blocks, kernel, threads, 0));
+  hp::require(blocks > 0, "GEMM kernel does not fit on a compute unit");
+  known.emplace(key, blocks);
+  return blocks;
+}
+
+// Whole tiles for every complete round of `slots` resident workgroups; the
+// tiles of an incomplete last round go to stream-K unless that round is
+// nearly full or K is too short to cut.
+Split plan_split(int64_t total, int64_t slices, int64_t slots) {
+  Split sp{};
+  sp.dp_tiles = total;
+  sp.slices = slices;
+  const int64_t rem = total % slots;
+  if (rem == 0 || 8 * rem >= 7 * slots || slices < 2 * kMinSlices) return sp;
+  sp.dp_tiles = total - rem;
+  const int64_t work = rem * slices;
+  sp.workers = std::min<int64_t>(slots, std::max<int64_t>(1, work / kMinSlices));
+  sp.base = work / sp.workers;
+  sp.extra = work % sp.workers;
+  // The kernels handle runs of at most one tile (two pieces): rem < slots
+  // gives base < slices when workers == slots, and base < 2 * kMinSlices <=
+  // slices otherwise.
+  if (sp.base + (sp.extra > 0 ? 1 : 0) > slices) hp::fail(HP_E_HIP, "internal: stream-K run longer than a tile");
+  return sp;
+}
+
+// Launches the whole-tile kernel over the complete rounds and, if tiles are
+// cut, the stream-K kernel and the fixup over a pooled workspace.
+template <typename T, int BM, int BN, typename Whole, typename Cut, typename Fix>
+void launch_split(hp_ctx* ctx, Whole whole, Cut cut, Fix fixup, int threads, const T* a, const T* b, T* c,
+                  int64_t m, int64_t n, int64_t k, const BatchDesc& bd, const TileMap& tm, int64_t bk,
+                  const char* name) {
+  const int per_cu = std::min(resident_per_cu(whole, threads), resident_per_cu(cut, threads));
+  Split sp = plan_split(tm.total, hp::ceil_div(k, bk), int64_t(ctx->compute_units) * per_cu);
+  if (sp.dp_tiles > 0) {
+    whole<<<sp.dp_tiles, threads, 0, ctx->stream>>>(a, b, c, m, n, k, bd, tm, sp);
+    hp::check_launch(name);
+  }
+  if (sp.workers > 0) {
+    sp.partial = hp::scratch_alloc(ctx, size_t(sp.workers) * 2 * BM * BN * sizeof(T));
+    cut<<<sp.workers, threads, 0, ctx->stream>>>(a, b, c, m, n, k, bd, tm, sp);
+    hp::check_launch(name);
+    fixup<<<(tm.total - sp.dp_tiles) * (BM * BN / 4 / 256), 256, 0, ctx->stream>>>(c, m, n, tm, sp);
+    hp::check_launch(name);
+    hp::scratch_free(ctx, sp.partial);
+  }
+}
+
+// Mode of a product: 0 interior, 1 M/N edges, 2 any K (see the kernels).
+int mode_of(int64_t m, int64_t n, int64_t k, int64_t bm, int64_t bn, int64_t bk) {
+  if (k % bk != 0) return 2;
+  return m % bm == 0 && n % bn == 0 ? 0 : 1;
+}
+
+template <bool TA, bool TB>
+void run_f32(hp_ctx* ctx, const float* a, const float* b, float* c, int64_t m, int64_t n, int64_t k,
+             const BatchDesc& bd, int64_t batch) {
+  using namespace f32;
+  TileMap tm;
+  prepare(m, n, batch, BM, BN, tm);
+  auto fix = fixup_kernel<float, hpd::f32x4, Layout>;
+  switch (mode_of(m, n, k, BM, BN, BK)) {
+    case 0:
+      launch_split<float, BM, BN>(ctx, kernel<0, false, TA, TB>, kernel<0, true, TA, TB>, fix, kThreads, a, b, c, m,
+                                  n, k, bd, tm, BK, "gemm_f32");
+      break;
+    case 1:
+      launch_split<float, BM, BN>(ctx, kernel<1, false, TA, TB>, kernel<1, true, TA, TB>, fix, kThreads, a, b, c, m,
+                                  n, k, bd, tm, BK, "gemm_f32");
+      break;
+    default:
+      launch_split<float, BM, BN>(ctx, kernel<2, false, TA, TB>, kernel<2, true, TA, TB>, fix, kThreads, a, b, c, m,
+                                  n, k, bd, tm, BK, "gemm_f32");
+  }
+}
+
+template <bool TA, bool TB>
+void run_f64(hp_ctx* ctx, const double* a, const double* b, double* c, int64_t m, int64_t n, int64_t k,
+             const BatchDesc& bd, int64_t batch) {
+  using namespace f64;
+  TileMap tm;
+  prepare(m, n, batch, BM, BN, tm);
+  auto fix = fixup_kernel<double, f64x4, Layout>;
+  switch (mode_of(m, n, k, BM, BN, BK)) {
+    case 0:
+      launch_split<double, BM, BN>(ctx, kernel<0, false, TA, TB>, kernel<0, true, TA, TB>, fix, kThreads, a, b, c,
+                                   m, n, k, bd, tm, BK, "gemm_f64");
+      break;
+    case 1:
+      launch_split<double, BM, BN>(ctx, kernel<1, false, TA, TB>, kernel<1, true, TA, TB>, fix, kThreads, a, b, c,
+                                   m, n, k, bd, tm, BK, "gemm_f64");
+      break;
+    default:
+      launch_split<double, BM, BN>(ctx, kernel<2, false, TA, TB>, kernel<2, true, TA, TB>, fix, kThreads, a, b, c,
+                                   m, n, k, bd, tm, BK, "gemm_f64");
+  }
+}
+
+}  // namespace

@@ -7,7 +7,11 @@ ExecutionPlan, then replays the plan on every call with fresh bindings.
 Grouping rules (reference _compiler.py:87-238), which decide what
 ``explain()["steps"]`` reports:
 - a matmul is its own step; with padding enabled and a backend padding plan it
-  becomes one ``padded_matmul`` step;
+  becomes one ``padded_matmul`` step; a matmul reading a private, full 2-D
+  transpose becomes one ``layout_matmul`` step on the untransposed operand
+  when the backend offers ``prepare_layout_matmul`` (reference :103-156);
+- ``b - A @ x`` with a private product becomes ``residual_matvec`` when the
+  lowerer accepts it (reference :157-176);
 - an elementwise node starts a ``fused`` group that inlines every elementwise
   producer used only by that group and not returned by the function;
 - a reduction of such a private elementwise producer becomes ``map_reduce``;
@@ -128,6 +132,19 @@ class ExecutionPlan:
     def _private(self, node):
         return self.uses[id(node)] <= 1 and id(node) not in self.output_ids
 
+    def _private_transpose(self, node):
+        """A gather that is exactly the full transpose of a 2-D array, used once."""
+        if node.op != "gather" or len(node.inputs) != 1 or len(node.shape) != 2 or not self._private(node):
+            return False
+        original = node.inputs[0]
+        return (
+            len(original.shape) == 2
+            and tuple(node.shape) == tuple(original.shape[::-1])
+            and node.dtype == original.dtype
+            and node.attrs.get("offset") == 0
+            and tuple(node.attrs.get("strides", ())) == (1, original.shape[1])
+        )
+
     def _add(self, node, kind, args, payload=None):
         self.steps.append((node, kind, tuple(args), payload))
         self._built.add(id(node))
@@ -168,6 +185,22 @@ class ExecutionPlan:
             if plan is not None:
                 self._ensure_all(node.inputs)
                 return self._add(node, "padded_matmul", node.inputs, plan)
+        prepare_layout = getattr(self.backend, "prepare_layout_matmul", None)
+        if node.op == "matmul" and prepare_layout is not None:
+            transposed = tuple(self._private_transpose(arg) for arg in node.inputs)
+            if any(transposed):
+                args = tuple(arg.inputs[0] if t else arg for arg, t in zip(node.inputs, transposed))
+                layout = prepare_layout(
+                    args[0].shape,
+                    args[1].shape,
+                    node.shape,
+                    node.dtype,
+                    transpose_a=transposed[0],
+                    transpose_b=transposed[1],
+                )
+                if layout is not None:
+                    self._ensure_all(args)
+                    return self._add(node, "layout_matmul", args, layout)
         if lowering is not None and node.op == "subtract" and node.inputs[1].op == "matmul":
             rhs, product = node.inputs
             matrix, vector = product.inputs
@@ -261,7 +294,7 @@ class ExecutionPlan:
             return backend.reduce(operands[0], node.attrs["axes"], node.attrs["keepdims"], node.dtype, **options)
         if kind == "matmul":
             return backend.matmul(*operands, node.shape, node.dtype)
-        if kind == "padded_matmul":
+        if kind in ("padded_matmul", "layout_matmul"):
             return payload.run(*operands)
         if kind == "norm":
             return backend.norm(operands[0], node.attrs["axes"], node.attrs["keepdims"], node.dtype)
@@ -283,6 +316,8 @@ class ExecutionPlan:
                 step["operation"] = node.attrs.get("operation", "sum")
             if kind == "padded_matmul":
                 step["padding"] = payload.explain()
+            if kind == "layout_matmul":
+                step["layout"] = payload.explain()
             steps.append(step)
         return {
             "backend": self.backend.name,

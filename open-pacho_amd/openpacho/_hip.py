@@ -4,7 +4,8 @@ Protocol (reference backends.py:82-150 and _cuda.py:129-679): ``name``,
 ``device``, ``fp64``, ``validate_dtype``, ``empty``, ``full``, ``upload``,
 ``download``, ``elementwise``, ``gather``, ``reduce``, ``matmul``, ``norm``,
 ``synchronize``, ``random_distributions``, ``random_data``, plus the optional
-``create_lowering``, ``prepare_padded_matmul``, ``residual_matvec``,
+``create_lowering``, ``prepare_padded_matmul``, ``prepare_layout_matmul``,
+``residual_matvec``,
 ``execution_scope``, ``release_cached_memory`` and ``close``.
 
 Storage is an _Allocation (device pointer + capacity) from the library's
@@ -402,6 +403,12 @@ class HIPBackend:
         from ._hip_gemv import residual_matvec_data
 
         return residual_matvec_data(self, a, x, b)
+
+    def prepare_layout_matmul(self, ashape, bshape, shape, dtype, *, transpose_a=False, transpose_b=False):
+        """Plan for a product of private 2-D transposes (plan step "layout_matmul")."""
+        from ._hip_layout import prepare
+
+        return prepare(self, ashape, bshape, shape, dtype, transpose_a=transpose_a, transpose_b=transpose_b)
 
     def prepare_padded_matmul(self, ashape, bshape, shape, dtype):
         from ._hip_padding import prepare

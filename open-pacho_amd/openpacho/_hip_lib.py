@@ -54,6 +54,7 @@ PROTOTYPES = {
     "hp_gather": [_ptr, _i32, _ptr, _ptr, _i64, _i32, _i64p, _i64p],
     "hp_pad_copy": [_ptr, _i32, _ptr, _ptr, _i64, _i64, _i64, _i64, _i64],
     "hp_gemm": [_ptr, _i32, _ptr, _ptr, _ptr, _i64, _i64, _i64, _i32, _i64p, _i64p, _i64p],
+    "hp_gemm_layout": [_ptr, _i32, _ptr, _ptr, _ptr, _i64, _i64, _i64, _i32, _i32],
     "hp_gemv": [_ptr, _i32, _ptr, _ptr, _ptr, _i64, _i64],
     "hp_gemv_residual": [_ptr, _i32, _ptr, _ptr, _ptr, _ptr, _i64, _i64],
     "hp_dot": [_ptr, _i32, _ptr, _ptr, _ptr, _i64],

@@ -363,3 +363,137 @@ def test_hip_lowering_residual_capability():
     assert not lowering.can_residual_matvec(batched, vector, rhs, node)
     backend.blas = "clblast"
     assert not lowering.can_residual_matvec(matrix, vector, rhs, node)
+
+
+# ---- layout plans for private transposes, reference tests/test_compiled_layout.py
+
+
+class _LayoutBackend(NumpyBackend):
+    """CPU backend offering hip layout plans, executed with NumPy."""
+
+    name = "test-layout"
+
+    def __init__(self):
+        self.gathers = 0
+        self.calls = []
+
+    def gather(self, *args):
+        self.gathers += 1
+        return super().gather(*args)
+
+    def download(self, array):
+        raise AssertionError("execution must not transfer to host")
+
+    def prepare_layout_matmul(self, ashape, bshape, shape, dtype, *, transpose_a=False, transpose_b=False):
+        from openpacho._hip_layout import prepare
+
+        plan = prepare(self, ashape, bshape, shape, dtype, transpose_a=transpose_a, transpose_b=transpose_b)
+        if plan is None:
+            return None
+        backend = self
+
+        class _NumpyRun:
+            explain = plan.explain
+
+            def run(self, a, b):
+                backend.calls.append((a.shape, b.shape, plan.transpose_a, plan.transpose_b))
+                left, right = a._data.reshape(a.shape), b._data.reshape(b.shape)
+                return ((left.T if plan.transpose_a else left) @ (right.T if plan.transpose_b else right)).ravel()
+
+        return _NumpyRun()
+
+
+@pytest.mark.parametrize("ta,tb", [(True, False), (False, True), (True, True)])
+@pytest.mark.parametrize("dtype", [np.float32, np.float64])
+def test_private_transpose_becomes_layout_step(ta, tb, dtype):
+    backend = _LayoutBackend()
+    rng = np.random.default_rng(42)
+    left = rng.normal(size=(7, 5) if ta else (5, 7)).astype(dtype)
+    right = rng.normal(size=(9, 7) if tb else (7, 9)).astype(dtype)
+    a, b = p.array(left, backend=backend), p.array(right, backend=backend)
+
+    @p.compile
+    def product(a, b):
+        return (a.T if ta else a) @ (b.T if tb else b)
+
+    prepared = product.prepare(a, b)
+    steps = prepared.explain()["steps"]
+    assert [s["kind"] for s in steps] == ["layout_matmul"]
+    layout = steps[0]["layout"]
+    assert layout["provider"] == "hip"
+    assert layout["leading_dimensions"] == (left.shape[1], right.shape[1], 9)
+    assert layout["transpose_operand_bytes"] == np.dtype(dtype).itemsize * (left.size * ta + right.size * tb)
+    for scale in (1, 2):
+        current = p.array(left * scale, backend=backend)
+        result = prepared(current, b)
+        expected = ((left * scale).T if ta else left * scale) @ (right.T if tb else right)
+        np.testing.assert_allclose(result._data.reshape(result.shape), expected, rtol=1e-6)
+    assert backend.gathers == 0
+    assert backend.calls == [(left.shape, right.shape, ta, tb)] * 2
+
+
+@pytest.mark.parametrize("public", [False, True])
+def test_shared_or_public_transpose_remains_materialized(public):
+    backend = _LayoutBackend()
+    host = np.arange(35, dtype=np.float32).reshape(7, 5)
+    a, b = p.array(host, backend=backend), p.array(host, backend=backend)
+
+    def source(a, b):
+        t = a.T
+        return (t @ b, t) if public else (t @ b, t + 1)
+
+    fn = p.compile(source)
+    actual = fn(a, b)
+    assert [s["kind"] for s in fn.explain(a, b)["steps"]].count("gather") == 1
+    assert not backend.calls and backend.gathers == 1
+    for result, reference in zip(actual, source(host, host)):
+        np.testing.assert_array_equal(result._data.reshape(result.shape), reference)
+
+
+@pytest.mark.parametrize("ashape,bshape", [((0, 5), (0, 9)), ((7, 0), (7, 9)), ((7, 5), (7, 0))])
+def test_layout_declines_empty_dimensions(ashape, bshape):
+    backend = _LayoutBackend()
+    a = p.array(np.zeros(ashape, dtype=np.float32), backend=backend)
+    b = p.array(np.zeros(bshape, dtype=np.float32), backend=backend)
+    result = p.compile(lambda a, b: a.T @ b)(a, b)
+    assert not backend.calls
+    np.testing.assert_array_equal(result._data.reshape(result.shape), np.zeros(ashape).T @ np.zeros(bshape))
+
+
+def test_layout_keeps_conversions_and_padding_precedence():
+    backend = _LayoutBackend()
+    a = p.array(np.arange(35, dtype=np.float32).reshape(7, 5), backend=backend)
+    b = p.array(np.arange(63, dtype=np.float64).reshape(7, 9), backend=backend)
+    fn = p.compile(lambda a, b: a.T @ b)
+    assert [s["kind"] for s in fn.explain(a, b)["steps"]] == ["gather", "cast", "matmul"]
+    one = p.array(np.ones((7, 5), dtype=np.float32), backend=backend)
+    square = p.compile(lambda a: a.T @ a)
+    assert [s["kind"] for s in square.explain(one)["steps"]] == ["layout_matmul"]  # one transpose, both sides
+    calls = []
+
+    class Padded:
+        def run(self, x, y):
+            calls.append("padding")
+            return backend.matmul(x, y, (5, 5), x.dtype)
+
+        def explain(self):
+            return {}
+
+    backend.prepare_padded_matmul = lambda *args: Padded()
+    p.compile(lambda a: a.T @ a, padding=True)(one)
+    assert calls == ["padding"] and not backend.calls
+
+
+def test_non_full_transpose_gather_is_not_folded():
+    from openpacho._compiler import ExecutionPlan
+    from openpacho._fusion import Expression, InputRef, TraceBackend
+
+    backend = _LayoutBackend()
+    for offset, strides, shape in [(1, (1, 5), (5, 7)), (0, (7, 1), (5, 7)), (0, (1, 5), (4, 7))]:
+        trace = TraceBackend(backend)
+        original = Expression(trace, (7, 5), np.float32, value=InputRef(0))
+        gather = trace.gather(original, shape, offset, strides)
+        right = Expression(trace, (7, 9), np.float32, value=InputRef(1))
+        product = trace.matmul(gather, right, (shape[0], 9), np.float32)
+        plan = ExecutionPlan(backend, (product,), False)
+        assert [s[1] for s in plan.steps] == ["gather", "matmul"]

@@ -333,3 +333,44 @@ def test_padding_preserves_special_values_and_signed_zero(hip):
         assert np.signbit(padded[index]) == np.signbit(ordinary[index])
         np.testing.assert_array_equal(padded[index], ordinary[index])
     np.testing.assert_array_equal(p.asnumpy(a), left)
+
+
+# ---- products of private transposes (hp_gemm_layout), reference
+# tests/test_clblast.py:410-440 and tests/test_compiled_layout.py:43-80
+
+LAYOUT_SHAPES = [(35, 33, 39), (300, 257, 129), (512, 1024, 768), (700, 2001, 517)]  # m, k, n
+
+
+@pytest.mark.parametrize("dtype", [np.float32, np.float64])
+@pytest.mark.parametrize("ta,tb", [(True, False), (False, True), (True, True)])
+@pytest.mark.parametrize("m,k,n", LAYOUT_SHAPES)
+def test_compiled_transpose_products_read_operands_in_place(hip, monkeypatch, dtype, ta, tb, m, k, n):
+    rng = np.random.default_rng(395 + m + k + n)
+    left = rng.uniform(-0.5, 0.5, (k, m) if ta else (m, k)).astype(dtype)
+    right = rng.uniform(-0.5, 0.5, (n, k) if tb else (k, n)).astype(dtype)
+    a, b = p.asarray(left, backend=hip), p.asarray(right, backend=hip)
+    replacement = p.asarray(left * 2, backend=hip)
+    compiled = p.compile(lambda a, b: (a.T if ta else a) @ (b.T if tb else b))
+    prepared = compiled.prepare(a, b)
+    steps = prepared.explain()["steps"]
+    assert [s["kind"] for s in steps] == ["layout_matmul"]
+    assert steps[0]["layout"]["provider"] == "hip"
+
+    def forbidden(*args, **kwargs):
+        raise AssertionError("private transpose product must not gather or download")
+
+    with monkeypatch.context() as context:
+        context.setattr(hip, "gather", forbidden)
+        context.setattr(hip, "download", forbidden)
+        result = prepared(a, b)
+        rebound = prepared(replacement, b)
+        hip.synchronize()
+    # Same tiles, K order and MFMA sequence as the materialized transposes.
+    eager = p.asnumpy((a.T if ta else a) @ (b.T if tb else b))
+    np.testing.assert_array_equal(p.asnumpy(result), eager)
+    op_a = (left.T if ta else left).astype(np.float64)
+    op_b = (right.T if tb else right).astype(np.float64)
+    scale = np.abs(op_a) @ np.abs(op_b)
+    bound = (4e-7 if dtype == np.float32 else 8e-16) * np.sqrt(k) * 4
+    assert np.all(np.abs(p.asnumpy(result) - op_a @ op_b) <= bound * scale + 1e-30)
+    assert np.all(np.abs(p.asnumpy(rebound) - 2 * (op_a @ op_b)) <= 2 * bound * scale + 1e-30)
