@@ -18,7 +18,7 @@ namespace {
 
 constexpr int kBlock = 256;
 constexpr int kLoads = 16;  // 16-byte loads per lane per chunk
-constexpr int kResidentGroupsPerCU = 8;
+constexpr int kResidentGroupsPerCU = 16;
 
 template <typename T>
 struct Traits;
@@ -216,8 +216,19 @@ __global__ __launch_bounds__(kBlock) void norm_merge_kernel(const T* __restrict_
   const int64_t begin = c * kMerge;
   const int64_t end = begin + kMerge < chunks ? begin + kMerge : chunks;
   const T* row = pairs + 2 * o * chunks;
+  // All of a thread's pairs are loaded before any merge: one memory round
+  // trip instead of one per pair (this kernel is latency-bound).
+  constexpr int kPer = int(kMerge / kBlock);
+  typedef T T2 __attribute__((ext_vector_type(2)));
+  T2 q[kPer];
+#pragma unroll
+  for (int j = 0; j < kPer; ++j) {
+    const int64_t i = begin + threadIdx.x + int64_t(j) * kBlock;
+    q[j] = i < end ? *reinterpret_cast<const T2*>(row + 2 * i) : T2{T(-INFINITY), T(0)};
+  }
   Pair<T> p = {T(-INFINITY), T(0)};
-  for (int64_t i = begin + threadIdx.x; i < end; i += kBlock) p = merge(p, Pair<T>{row[2 * i], row[2 * i + 1]});
+#pragma unroll
+  for (int j = 0; j < kPer; ++j) p = merge(p, Pair<T>{q[j][0], q[j][1]});
   p = wave_merge(p);
   const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
   if (lane == 0) {
