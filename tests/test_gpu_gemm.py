@@ -374,3 +374,46 @@ def test_compiled_transpose_products_read_operands_in_place(hip, monkeypatch, dt
     bound = (4e-7 if dtype == np.float32 else 8e-16) * np.sqrt(k) * 4
     assert np.all(np.abs(p.asnumpy(result) - op_a @ op_b) <= bound * scale + 1e-30)
     assert np.all(np.abs(p.asnumpy(rebound) - 2 * (op_a @ op_b)) <= 2 * bound * scale + 1e-30)
+
+
+# ---- exactly representable accumulation and special values, reference
+# tests/test_rectangular_gemm.py:62-104
+
+
+@pytest.mark.parametrize("m,k,n", [(33, 4081, 257), (65, 4095, 1023), (95, 8191, 2051)])
+def test_dyadic_products_are_exact_and_rebinding_is_copy_free(hip, monkeypatch, m, k, n):
+    rng = np.random.default_rng(613)
+    # Multiples of 1/256 with |sum| < 2^7: every partial sum is exact in fp32,
+    # so any K order gives the float64 result bit for bit.
+    host = [rng.integers(-2, 3, shape).astype("float32") / 16 for shape in ((m, k), (k, n))]
+    a, b = (p.asarray(h, backend=hip) for h in host)
+    twice_a = p.asarray(host[0] * 2, backend=hip)
+    baseline = p.asnumpy(a @ b)
+    compiled = p.compile(lambda a, b: a @ b).prepare(a, b)
+    with monkeypatch.context() as guard:
+        guard.setattr(hip, "download", lambda *args: pytest.fail("Hidden download"))
+        guard.setattr(hip, "gather", lambda *args: pytest.fail("Unexpected packing/crop"))
+        first, second = compiled(a, b), compiled(twice_a, b)
+    np.testing.assert_array_equal(p.asnumpy(first).view("uint32"), baseline.view("uint32"))
+    np.testing.assert_array_equal(p.asnumpy(first), host[0].astype("float64") @ host[1])
+    np.testing.assert_array_equal(p.asnumpy(second), baseline * 2)
+    assert first._data is not second._data
+
+
+@pytest.mark.parametrize("dtype", [np.float32, np.float64])
+def test_special_values_and_subnormals_propagate(hip, dtype):
+    left = np.zeros((33, 4081), dtype=dtype)
+    right = np.zeros((4081, 257), dtype=dtype)
+    tiny = np.nextafter(dtype(0), dtype(1))
+    left[0, 0], left[1, 0], left[2, 0] = np.inf, np.nan, tiny
+    left[3, 0], left[3, 1] = np.finfo(dtype).max, np.finfo(dtype).max  # overflow to inf
+    right[0, :3] = [0, 1, -1]
+    right[1, :3] = [0, 1, 1]
+    got = p.asnumpy(p.asarray(left, backend=hip) @ p.asarray(right, backend=hip))
+    with np.errstate(all="ignore"):
+        want = left.astype(np.float64) @ right.astype(np.float64)
+    want = want.astype(dtype)
+    np.testing.assert_array_equal(np.isnan(got), np.isnan(want))
+    finite = ~np.isnan(want)
+    np.testing.assert_array_equal(got[finite], want[finite])
+    assert got[2, 1] == tiny and got[2, 2] == -tiny  # subnormals are not flushed
