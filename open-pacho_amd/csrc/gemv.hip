@@ -133,18 +133,47 @@ __global__ __launch_bounds__(kBlock) void gemv_short_kernel(const T* __restrict_
   if (lane == 0) y[row] = rhs ? rhs[row] - acc : acc;
 }
 
-// Dot product: each workgroup reduces one chunk; partials are summed by a
-// single workgroup in index order (deterministic).
+// Dot product: each 1024-thread workgroup reduces one chunk of kDotChunk
+// elements; partials are summed by a single workgroup in index order
+// (deterministic). A full, aligned chunk is read with all of its 16-byte loads
+// in flight at once (one memory round trip), so a 16384-element dot is one
+// short launch.
+constexpr int kDotThreads = 1024;
 constexpr int64_t kDotChunk = 16384;
 
 template <typename T>
-__global__ __launch_bounds__(kBlock) void dot_kernel(const T* __restrict__ x, const T* __restrict__ z,
-                                                     T* __restrict__ out, int64_t n) {
+__global__ __launch_bounds__(kDotThreads) void dot_kernel(const T* __restrict__ x, const T* __restrict__ z,
+                                                         T* __restrict__ out, int64_t n, bool aligned) {
+  using V = typename Vec<T>::type;
+  constexpr int W = Vec<T>::width;
+  constexpr int kPer = int(kDotChunk / W / kDotThreads);
   const int64_t begin = int64_t(blockIdx.x) * kDotChunk;
-  const int64_t end = begin + kDotChunk < n ? begin + kDotChunk : n;
-  T acc[1] = {T(0)};
-  for (int64_t i = begin + threadIdx.x; i < end; i += kBlock) acc[0] = dfma(x[i], z[i], acc[0]);
-  block_reduce_store<T, 1>(acc, out, blockIdx.x, gridDim.x);
+  const int64_t len = n - begin < kDotChunk ? n - begin : kDotChunk;
+  T acc = T(0);
+  if (aligned && len == kDotChunk) {
+    const V* xv = reinterpret_cast<const V*>(x + begin);
+    const V* zv = reinterpret_cast<const V*>(z + begin);
+    V xs[kPer], zs[kPer];
+#pragma unroll
+    for (int j = 0; j < kPer; ++j) {
+      xs[j] = xv[threadIdx.x + j * kDotThreads];
+      zs[j] = zv[threadIdx.x + j * kDotThreads];
+    }
+#pragma unroll
+    for (int j = 0; j < kPer; ++j) acc = dot_vec(xs[j], zs[j], acc);
+  } else {
+    for (int64_t i = threadIdx.x; i < len; i += kDotThreads) acc = dfma(x[begin + i], z[begin + i], acc);
+  }
+  __shared__ T partial[kDotThreads / 64];
+  const T s = hpd::wave_sum(acc);
+  if ((threadIdx.x & 63) == 0) partial[threadIdx.x >> 6] = s;
+  __syncthreads();
+  if (threadIdx.x == 0) {
+    T total = partial[0];
+#pragma unroll
+    for (int w = 1; w < kDotThreads / 64; ++w) total += partial[w];
+    out[blockIdx.x] = total;
+  }
 }
 
 template <typename T>
@@ -178,13 +207,14 @@ template <typename T>
 void run_dot(hp_ctx* ctx, const T* x, const T* z, T* out, int64_t n) {
   const int64_t chunks = hp::ceil_div(n, kDotChunk);
   hp::require(chunks <= hp::kMaxGrid, "dot too long for one launch");
+  const bool aligned = reinterpret_cast<uintptr_t>(x) % 16 == 0 && reinterpret_cast<uintptr_t>(z) % 16 == 0;
   if (chunks == 1) {
-    dot_kernel<T><<<1, kBlock, 0, ctx->stream>>>(x, z, out, n);
+    dot_kernel<T><<<1, kDotThreads, 0, ctx->stream>>>(x, z, out, n, aligned);
     hp::check_launch("dot");
     return;
   }
   T* partial = static_cast<T*>(hp::scratch_alloc(ctx, size_t(chunks) * sizeof(T)));
-  dot_kernel<T><<<chunks, kBlock, 0, ctx->stream>>>(x, z, partial, n);
+  dot_kernel<T><<<chunks, kDotThreads, 0, ctx->stream>>>(x, z, partial, n, aligned);
   hp::check_launch("dot");
   sum_partials_kernel<T><<<1, kBlock, 0, ctx->stream>>>(partial, out, chunks);
   hp::check_launch("dot partials");
