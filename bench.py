@@ -227,7 +227,7 @@ def bench_extras(p, hip, only, skip_cpu):
                 "unit": "Gsample/s",
                 "kernel_us": round(ms * 1e3, 2),
                 "roofline": roofline("hbm", bytes_moved, ms, _traffic(f"rng_{dist}")),
-                "alu_bound_note": "20 32x32->64 integer multiplies per Philox4x32-10 block, one block per sample",
+                "alu_bound_note": "vector-ALU issue bound: one Philox4x32-10 block per sample = ~17 v_mad_u64_u32 + ~17 three-input XORs (v_bitop3_b32) per sample",
             }
         if not skip_cpu:
             count = 1 << 22

@@ -4,12 +4,15 @@
 // Stream contract: reference _random.py:19-31 (rounds), :43-45 / :73-77 (unit
 // conversion), :50-56 / :93-102 (transforms), _random_cuda.py:10-28.
 //
-// Throughput is bound by the 32x32->64 integer multiplies (two per round).
-// Each thread produces four consecutive elements for instruction-level
-// parallelism and 16-byte stores. When a wave's 256 counters share their high
+// Throughput is bound by vector ALU issue, not HBM: per element about 17
+// 32x32->64 multiplies (v_mad_u64_u32) and as many three-input XORs, each a
+// full wave64 instruction. Each thread produces four consecutive elements for
+// instruction-level parallelism and 16-byte stores. When a wave's 256 counters share their high
 // 32-bit word, that word lives in a scalar register: round 1 then needs one
 // vector multiply (its c2 input is zero) and round 2's c0 product is a scalar
 // multiply, saving 2 of the 20 vector multiplies per element.
+#include <cmath>
+
 #include "common.h"
 
 namespace {
@@ -23,14 +26,21 @@ struct Words {
   uint32_t x0, x1, x2, x3;
 };
 
+// a ^ b ^ c as one gfx950 v_bitop3_b32 (truth table 0x96 is the 3-input
+// parity); the compiler otherwise emits two v_xor_b32, and the XORs then cost
+// as many VALU cycles as the multiplies.
+__device__ __forceinline__ uint32_t xor3(uint32_t a, uint32_t b, uint32_t c) {
+  return __builtin_amdgcn_bitop3_b32(a, b, c, 0x96);
+}
+
 __device__ __forceinline__ Words philox10(uint32_t c0, uint32_t c1, uint32_t c2, uint32_t c3, uint32_t k0,
                                           uint32_t k1) {
 #pragma unroll
   for (int round = 0; round < 10; ++round) {
     const uint64_t p0 = uint64_t(c0) * kM0;
     const uint64_t p1 = uint64_t(c2) * kM1;
-    const uint32_t n0 = uint32_t(p1 >> 32) ^ c1 ^ k0;
-    const uint32_t n2 = uint32_t(p0 >> 32) ^ c3 ^ k1;
+    const uint32_t n0 = xor3(uint32_t(p1 >> 32), c1, k0);
+    const uint32_t n2 = xor3(uint32_t(p0 >> 32), c3, k1);
     c0 = n0;
     c1 = uint32_t(p1);
     c2 = n2;
@@ -84,19 +94,53 @@ __device__ __forceinline__ T transform(const Words& w, T first, T second, T uppe
 // relative error 9e-8. Against the reference's libm transforms this stays far
 // inside the 3e-6 tolerance of the float32 stream contract, and replaces ~100
 // instructions of log1pf/cosf/sqrtf per sample with ~6.
+//
+// log2(1 - u) <= 0 on the grid, so -log(1 - u) is written |log2(1 - u)| * ln 2.
+// At u = 0 this is +0, as -log1p(-0) is; the form 0 - log2(1 - u) * ln 2 was
+// turned into a negation by the code generator and gave -0 there.
+__device__ __forceinline__ float neg_log1m_grid(float u) {
+  return __builtin_fabsf(__builtin_amdgcn_logf(1.0f - u)) * 0.693147180559945309417f;
+}
+
 template <>
 __device__ __forceinline__ float transform<float, HP_NORMAL>(const Words& w, float first, float second, float) {
   const float u = unit<float>(w.x0, w.x1);
-  const float nl = 0.0f - __builtin_amdgcn_logf(1.0f - u) * 0.693147180559945309417f;
+  // 2 * (|log2(1 - u)| * ln2) == |log2(1 - u)| * (2 * ln2) exactly: doubling
+  // commutes with rounding, so the factor 2 costs no instruction.
+  const float two_nl = __builtin_fabsf(__builtin_amdgcn_logf(1.0f - u)) * (2.0f * 0.693147180559945309417f);
   const float v = unit<float>(w.x2, w.x3);
-  return first + second * (__builtin_amdgcn_sqrtf(2.0f * nl) * __builtin_amdgcn_cosf(v));
+  return first + second * (__builtin_amdgcn_sqrtf(two_nl) * __builtin_amdgcn_cosf(v));
 }
 
 template <>
 __device__ __forceinline__ float transform<float, HP_EXPONENTIAL>(const Words& w, float, float second, float) {
   const float u = unit<float>(w.x0, w.x1);
-  const float nl = 0.0f - __builtin_amdgcn_logf(1.0f - u) * 0.693147180559945309417f;
+  const float nl = neg_log1m_grid(u);
   return second * nl;
+}
+
+// Uniform with the width pre-scaled by the unit's power of two, selected by
+// the host when that scaling is exact (see uniform_scaled). The unit numerator
+// k (float32: word0 >> 8; float64: the 53-bit integer) is exact in T, so
+// k * (width * 2^-b) and (k * 2^-b) * width are the same real product and
+// round to the same value: one multiply per sample fewer, bit for bit.
+constexpr int kUniformScaled = 4;
+
+template <>
+__device__ __forceinline__ float transform<float, kUniformScaled>(const Words& w, float first, float scaled,
+                                                                  float upper) {
+  const float value = first + float(w.x0 >> 8) * scaled;
+  // first <= upper, value is finite and neither bound is -0 (host check), so
+  // the median of three is the reference clamp to [first, upper].
+  return __builtin_amdgcn_fmed3f(value, first, upper);
+}
+
+template <>
+__device__ __forceinline__ double transform<double, kUniformScaled>(const Words& w, double first, double scaled,
+                                                                    double upper) {
+  const double k = double(w.x0 >> 5) * 67108864.0 + double(w.x1 >> 6);
+  const double value = first + k * scaled;
+  return value < first ? first : (value > upper ? upper : value);
 }
 
 template <typename T>
@@ -173,11 +217,31 @@ __global__ __launch_bounds__(kBlock) void philox_words_kernel(uint32_t* __restri
   reinterpret_cast<uint4*>(out)[i] = q;
 }
 
+// The pre-scaled uniform applies when width * 2^-b is exact (no underflow)
+// and, for the float32 median clamp, neither bound is -0: then the sample
+// first + width * u is never -0 and med3 orders exactly like the comparisons.
+template <typename T>
+bool uniform_scaled(T first, T second, T upper, T* scaled) {
+  const int bits = sizeof(T) == 4 ? 24 : 53;
+  const T width = second - first;
+  *scaled = std::ldexp(width, -bits);
+  if (!std::isfinite(width) || std::ldexp(*scaled, bits) != width) return false;
+  if (sizeof(T) == 4 && ((first == 0 && std::signbit(first)) || (upper == 0 && std::signbit(upper)))) return false;
+  return true;
+}
+
 template <typename T>
 void launch(hp_ctx* ctx, int dist, T* out, int64_t count, uint32_t k0, uint32_t k1, uint64_t start, T first,
             T second, T upper) {
   const int64_t grid = hp::ceil_div(count, kBlock * kPerThread);
   hp::require(grid <= hp::kMaxGrid, "random output too large for one launch");
+  T scaled;
+  if (dist == HP_UNIFORM && uniform_scaled(first, second, upper, &scaled)) {
+    philox_kernel<T, kUniformScaled><<<grid, kBlock, 0, ctx->stream>>>(out, count, k0, k1, start, first, scaled,
+                                                                       upper);
+    hp::check_launch("philox");
+    return;
+  }
   switch (dist) {
     case HP_RANDOM:
       philox_kernel<T, HP_RANDOM><<<grid, kBlock, 0, ctx->stream>>>(out, count, k0, k1, start, first, second, upper);

@@ -65,6 +65,53 @@ def test_transcendental_transforms_within_reference_tolerance(hip, dtype, dist):
         np.testing.assert_allclose(got, want, rtol=tol, atol=tol)
 
 
+# Seed 42 draws the float32 unit u = 0 (word0 >> 8 == 0) at these counters,
+# where -log1p(-0) = +0: exponential gives +0 and normal gives loc + scale * (+0 * cos).
+ZERO_UNIT_COUNTERS = (25077234, 26967075)
+
+
+@pytest.mark.parametrize("dist,first,second", [("exponential", 0.0, 2.0), ("normal", -0.0, 3.0), ("normal", 0.0, 3.0)])
+def test_zero_unit_sample_has_the_reference_signed_zero(hip, dist, first, second):
+    for counter in ZERO_UNIT_COUNTERS:
+        assert philox.c_words(1, 42, counter)[0, 0] >> 8 == 0
+        rng = p.random.default_rng(42, backend=hip)
+        rng._counter = counter - 2
+        kwargs = {"scale": second} if dist == "exponential" else {"loc": first, "scale": second}
+        got = p.asnumpy(getattr(rng, dist)(size=5, dtype="float32", **kwargs))
+        want = nb.random(dist, "float32", (5,), 42, counter - 2, first, second)
+        assert got[2] == 0 and want[2] == 0
+        np.testing.assert_array_equal(np.signbit(got), np.signbit(want), err_msg=f"{dist} counter={counter}")
+        np.testing.assert_allclose(got, want, rtol=3e-6, atol=3e-6)
+
+
+# Bounds that select each uniform kernel: a pre-scaled width with a median
+# clamp where width * 2^-24 (2^-53) is exact and no bound is -0, the plain
+# first + width * u with comparisons otherwise (signed zeros, subnormal widths).
+UNIFORM_BOUNDS = [
+    (-3.0, 7.0),
+    (0.0, 1.0),
+    (-0.0, 1.0),
+    (0.0, 0.0),
+    (-0.0, 0.0),
+    (0.0, -0.0),
+    (1.0, 1.0 + 2.0**-23),
+    (1e-38, 3e-38),
+    (-1.5e38, 1.5e38),
+    (5e-324, 1e-322),
+    (-2.0**-126, 2.0**-126),
+]
+
+
+@pytest.mark.parametrize("dtype", ["float32", "float64"])
+@pytest.mark.parametrize("low,high", UNIFORM_BOUNDS)
+def test_uniform_bounds_are_bit_exact_on_both_kernels(hip, dtype, low, high):
+    rng = p.random.default_rng(7, backend=hip)
+    rng._counter = 2**32 - 1000
+    got = p.asnumpy(rng.uniform(low, high, size=4099, dtype=dtype))
+    want = philox.c_uniform(dtype, 4099, 7, 2**32 - 1000, "uniform", low, high)
+    np.testing.assert_array_equal(got.view(f"u{got.itemsize}"), want.view(f"u{want.itemsize}"))
+
+
 def test_matches_reference_numpy_backend_golden_samples(hip):
     with np.load(GOLDEN) as data:
         golden = {k: data[k] for k in data.files}
