@@ -37,7 +37,13 @@ __global__ void gather_kernel(const T* __restrict__ src, T* __restrict__ dst, in
   }
 }
 
-// One workgroup per destination row (grid-stride over rows); lanes walk columns.
+// One workgroup per destination row (grid-stride over rows); lanes walk
+// columns. Each lane issues kPadUnroll loads before its stores, so a row of a
+// few thousand elements is one or two rounds of independent loads rather than
+// a chain of load-store pairs. Rows of padded operands are rarely 16-byte
+// aligned on both sides, so accesses stay element-wide (coalesced per wave).
+constexpr int kPadUnroll = 8;
+
 template <typename T>
 __global__ void pad_kernel(const T* __restrict__ src, T* __restrict__ dst, int64_t rows_total, int64_t src_rows,
                            int64_t src_cols, int64_t dst_rows, int64_t dst_cols) {
@@ -45,12 +51,22 @@ __global__ void pad_kernel(const T* __restrict__ src, T* __restrict__ dst, int64
     const int64_t b = row / dst_rows;
     const int64_t r = row - b * dst_rows;
     T* out = dst + row * dst_cols;
-    if (r < src_rows) {
-      const T* in = src + (b * src_rows + r) * src_cols;
-      const int64_t copy_cols = src_cols < dst_cols ? src_cols : dst_cols;
-      for (int64_t c = threadIdx.x; c < dst_cols; c += blockDim.x) out[c] = c < copy_cols ? in[c] : T(0);
-    } else {
-      for (int64_t c = threadIdx.x; c < dst_cols; c += blockDim.x) out[c] = T(0);
+    const bool from_src = r < src_rows;
+    const T* in = src + (from_src ? (b * src_rows + r) * src_cols : 0);
+    const int64_t copy_cols = from_src ? (src_cols < dst_cols ? src_cols : dst_cols) : 0;
+    const int64_t step = int64_t(blockDim.x) * kPadUnroll;
+    for (int64_t base = threadIdx.x; base < dst_cols; base += step) {
+      T v[kPadUnroll];
+#pragma unroll
+      for (int j = 0; j < kPadUnroll; ++j) {
+        const int64_t c = base + int64_t(j) * blockDim.x;
+        v[j] = c < copy_cols ? in[c] : T(0);
+      }
+#pragma unroll
+      for (int j = 0; j < kPadUnroll; ++j) {
+        const int64_t c = base + int64_t(j) * blockDim.x;
+        if (c < dst_cols) out[c] = v[j];
+      }
     }
   }
 }
