@@ -389,13 +389,17 @@ __global__ __launch_bounds__(kThreads, 1) void kernel(const float* __restrict__ 
     const int64_t worker = xcd_major(blockIdx.x, sp.workers);
     const int64_t g = sk_begin(sp, worker), g_end = sk_begin(sp, worker + 1);
     // A run is at most one tile long: the end of one tile and the start of
-    // the next at most.
+    // the next at most. The start of the next tile goes first: every worker
+    // then sits at K slice tau (first piece) or slices - run + tau (second
+    // piece) at time tau, so workers sharing an XCD read the same A and B
+    // slices together and its L2 serves them, as in the whole-tile kernel
+    // (in run order the K positions of neighbouring workers all differ).
     const int64_t t0 = g / sp.slices;
     const int64_t s0 = g - t0 * sp.slices;
     const int64_t s1 = g_end - t0 * sp.slices < sp.slices ? g_end - t0 * sp.slices : sp.slices;
-    piece(sp.dp_tiles + t0, s0, s1, s0 == 0 && s1 == sp.slices ? -1 : worker * 2);
     const int64_t rest = g_end - (t0 + 1) * sp.slices;
     if (rest > 0) piece(sp.dp_tiles + t0 + 1, 0, rest, rest == sp.slices ? -1 : worker * 2 + 1);
+    piece(sp.dp_tiles + t0, s0, s1, s0 == 0 && s1 == sp.slices ? -1 : worker * 2);
   }
 }
 
@@ -567,9 +571,10 @@ __global__ __launch_bounds__(kThreads, 1) void kernel(const double* __restrict__
     const int64_t t0 = g0 / sp.slices;
     const int64_t s0 = g0 - t0 * sp.slices;
     const int64_t s1 = g_end - t0 * sp.slices < sp.slices ? g_end - t0 * sp.slices : sp.slices;
-    piece(sp.dp_tiles + t0, s0, s1, s0 == 0 && s1 == sp.slices ? -1 : worker * 2);
+    // Start of the next tile first, as in the f32 kernel (L2 sharing).
     const int64_t rest = g_end - (t0 + 1) * sp.slices;
     if (rest > 0) piece(sp.dp_tiles + t0 + 1, 0, rest, rest == sp.slices ? -1 : worker * 2 + 1);
+    piece(sp.dp_tiles + t0, s0, s1, s0 == 0 && s1 == sp.slices ? -1 : worker * 2);
   }
 }
 
