@@ -85,6 +85,22 @@ def _traffic(name):
         return None
 
 
+# Vector-ALU issue peak: 256 CUs x 4 SIMDs x 16 lanes x 2.4 GHz, in lane
+# instructions per second (a wave64 instruction occupies a SIMD 4 cycles).
+PEAK_VALU_TINSTR = 256 * 4 * 16 * 2.4e9 / 1e12
+
+
+def _valu(name, samples, ms):
+    """Vector-ALU roofline of an RNG kernel from its PMC instruction count (profiles/valu.json)."""
+    path = ROOT / "profiles" / "valu.json"
+    try:
+        per_sample = json.loads(path.read_text())[name]["valu_instr_per_sample"]
+    except (OSError, ValueError, KeyError):
+        return None
+    achieved = per_sample * samples / (ms * 1e-3) / 1e12
+    return {"bound": "valu", "instr_per_sample": per_sample, "achieved": round(achieved, 2), "peak": round(PEAK_VALU_TINSTR, 2), "unit": "Tinstr/s", "frac": round(achieved / PEAK_VALU_TINSTR, 4)}
+
+
 def cpu_threads():
     try:
         return len(os.sched_getaffinity(0))
@@ -227,6 +243,7 @@ def bench_extras(p, hip, only, skip_cpu):
                 "unit": "Gsample/s",
                 "kernel_us": round(ms * 1e3, 2),
                 "roofline": roofline("hbm", bytes_moved, ms, _traffic(f"rng_{dist}")),
+                "valu_roofline": _valu(f"rng_{dist}", n, ms),
                 "alu_bound_note": "vector-ALU issue bound: one Philox4x32-10 block per sample = ~17 v_mad_u64_u32 + ~17 three-input XORs (v_bitop3_b32) per sample",
             }
         if not skip_cpu:
