@@ -38,8 +38,27 @@ ELEMENTWISE = frozenset({f.__name__ for f in UFUNCS.values()} | {"cast", "where"
 _DYNAMIC_SCALARS = (int, float, bool, np.generic)
 
 
+# NumPy functions implemented in C expose no signature on some NumPy releases
+# (np.where on 2.2); compile/fuse bind them by their documented parameters.
+_BUILTIN_SIGNATURES = {
+    np.where: inspect.Signature(
+        [inspect.Parameter(name, inspect.Parameter.POSITIONAL_ONLY) for name in ("condition", "x", "y")]
+    ),
+}
+
+
+def _signature_of(function):
+    try:
+        return inspect.signature(function)
+    except ValueError:
+        try:
+            return _BUILTIN_SIGNATURES[function]
+        except (KeyError, TypeError):
+            raise TypeError(f"compile cannot bind the arguments of {function!r}") from None
+
+
 def _bind(function, args, kwargs, signature=None):
-    signature = signature or inspect.signature(function)
+    signature = signature or _signature_of(function)
     if any(p.kind in (p.VAR_KEYWORD, p.VAR_POSITIONAL) for p in signature.parameters.values()):
         raise TypeError("compile requires named parameters, without *args or **kwargs")
     bound = signature.bind(*args, **kwargs)
@@ -352,7 +371,7 @@ class CompiledFunction:
         if isinstance(static_argnames, str):
             static_argnames = (static_argnames,)
         self.static_argnames = tuple(static_argnames)
-        signature = inspect.signature(function)
+        signature = _signature_of(function)
         if not set(self.static_argnames) <= set(signature.parameters):
             raise ValueError("static_argnames contains an unknown parameter")
         if not isinstance(cache_size, int) or cache_size < 1:

@@ -302,12 +302,17 @@ class HIPBackend:
         dtype = self.validate_dtype(dtype)
         if operation not in lib_.REDUCTIONS:
             raise ValueError(f"Unknown reduction operation: {operation}")
-        if dtype.kind == "b" and operation == "sum":
-            raise NotImplementedError("Boolean sum requires a numeric accumulator dtype")
+        boolean_sum = dtype.kind == "b" and operation == "sum"
+        if boolean_sum:
+            # NumPy's sum in bool is a logical or (so are the reference's OpenCL
+            # kernels, _opencl.py:340-341): max over 0/1 bytes, False if empty.
+            operation = "max"
         if a.dtype != dtype:
             cast = self.elementwise("cast", [a], a.shape, dtype)
             a = ndarray._wrap(cast, a.shape, dtype, self)
         source, outer, reduced, inner = self._rows_view(a, axes)
+        if boolean_sum and not reduced:
+            return self.full((outer * inner,), False, dtype)
         out = self.empty((outer * inner,), dtype)
         if outer * inner:
             with self._active():

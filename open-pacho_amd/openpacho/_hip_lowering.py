@@ -340,7 +340,7 @@ class HIPLowering:
     def prepare_map_reduce(self, node, group, leaves):
         operation = node.attrs.get("operation", "sum")
         if node.dtype.kind == "b" and operation == "sum":
-            raise NotImplementedError("Boolean sum requires a numeric accumulator dtype")
+            operation = "max"  # a sum in bool is a logical or (HIPBackend.reduce)
         mapped = node.inputs[0]
         if prod(mapped.shape) > 2**31 - 1:
             raise ValueError("Array exceeds GPU indexing limits")

@@ -151,10 +151,24 @@ def test_inlined_product_stays_a_matmul_and_threads_rebind(hip, monkeypatch):
     assert len(calls) == 4
 
 
-def test_boolean_accumulator_is_explicitly_unsupported(hip):
-    host = np.array([0.0, 2.0, -1.0, 0.0, 5.0], np.float32)
+@pytest.mark.parametrize("shape,axis", [((5,), None), ((3, 20001), 1), ((20001, 3), 0), ((4, 0), 1), ((0, 4), 0)])
+def test_boolean_accumulator_is_a_logical_or(hip, shape, axis):
+    # NumPy sums in bool as a logical or, as the reference's OpenCL kernels do
+    # (its initial CUDA backend rejects the case); eager and compiled agree.
+    host = np.random.default_rng(3).choice(np.array([0, 0, 0, 2, -1, np.nan], np.float32), size=shape)
+    if host.size and axis == 1:
+        host[0, :] = 0  # an all-false row
+    if host.size and axis == 0:
+        host[:, 0] = 0
     a = p.asarray(host, backend=hip)
-    with pytest.raises(NotImplementedError, match="Boolean sum"):
-        p.compile(lambda a: np.sum(a > 0, dtype=np.bool_))(a)
-    counted = p.compile(lambda a: np.sum(a > 0))(a)  # numeric accumulator: supported
-    assert p.asnumpy(counted) == 2 and counted.dtype == np.sum(host > 0).dtype
+    want = np.sum(host > 0, axis=axis, dtype=np.bool_)
+    eager = p.sum(a > 0, axis=axis, dtype=np.bool_)
+    compiled = p.compile(lambda a: np.sum(a > 0, axis=axis, dtype=np.bool_))
+    for got in (eager, compiled(a)):
+        assert got.dtype == np.bool_ and got.shape == want.shape
+        np.testing.assert_array_equal(p.asnumpy(got), want)
+    nonzero = p.compile(lambda a: np.sum(a, axis=axis, dtype=np.bool_))(a)  # NaN counts as true
+    np.testing.assert_array_equal(p.asnumpy(nonzero), np.sum(host, axis=axis, dtype=np.bool_))
+    counted = p.compile(lambda a: np.sum(a > 0, axis=axis))(a)  # numeric accumulator
+    np.testing.assert_array_equal(p.asnumpy(counted), np.sum(host > 0, axis=axis))
+    assert counted.dtype == np.sum(host > 0, axis=axis).dtype
