@@ -8,8 +8,10 @@ inputs, thread sharing, rejected mutation and nesting), tests/test_fusion.py:7-1
 arguments, one launch per fused group, rejected control flow, scalar overflow,
 intermediate rounding, a pool that keeps queued inputs), tests/test_prepared.py:25-70
 (rebinding, specialization checks) and tests/test_irregular_workloads.py:41-95
-(odd and rectangular tile boundaries, GEMV residual with axis reductions).
-The same body runs on the NumPy backend (CPU tier) and on hip (``gpu``).
+(odd and rectangular tile boundaries, GEMV residual with axis reductions) and
+tests/test_compiler_optimization.py:19-90 (mapped reductions over every dtype,
+axes and empty shapes; a bool accumulator; shared intermediates). The same
+body runs on the NumPy backend (CPU tier) and on hip (``gpu``).
 """
 
 import gc
@@ -269,6 +271,52 @@ def test_compile_cache_separates_backends_and_rejects_mixing(hip):
         p.compile(lambda a, b: a + b)(numpy_array, hip_array)
     with pytest.raises(p.BackendMismatchError):
         p.fuse(lambda a: a + hip_array)(numpy_array)
+
+
+# ---- mapped reductions (reference tests/test_compiler_optimization.py) ------------------
+
+
+@pytest.mark.parametrize("dtype", [np.float32, np.float64, np.int32, np.uint32, np.bool_])
+@pytest.mark.parametrize(
+    "shape,axes",
+    [
+        ((4099,), None),
+        ((5, 32), (-1,)),
+        ((3, 2, 33), (1, 2)),
+        ((9, 7, 39), (0, 2)),
+        ((67, 3, 69), (0, 2)),
+        ((2, 3), ()),
+        ((), None),
+        ((2, 0, 3), (1,)),
+        ((0, 4097), (1,)),
+    ],
+)
+def test_compiled_mapped_reduction(backend, dtype, shape, axes):
+    host = (np.arange(int(np.prod(shape))) % 7).astype(dtype).reshape(shape)
+
+    @p.compile
+    def total(a):
+        mapped = a == 1 if dtype is np.bool_ else a * a + 2
+        return np.sum(mapped, axis=axes, keepdims=True)
+
+    mapped = host == 1 if dtype is np.bool_ else host * host + 2
+    _result(total(_array(host, backend)), np.sum(mapped, axis=axes, keepdims=True), rtol=3e-5, atol=3e-5)
+
+
+def test_map_boolean_accumulator_and_shared_intermediate(backend):
+    host = np.zeros(9001, dtype=np.int32)
+    host[-1] = 1
+    compiled = p.compile(lambda a: np.sum(a > 0, dtype=np.bool_))
+    _result(compiled(_array(host, backend)), np.sum(host > 0, dtype=np.bool_))
+    values = np.arange(4133, dtype=np.float32) / 1000
+
+    @p.compile
+    def shared(a):
+        x = a + 2
+        return x, np.sum(x * x), x - 1
+
+    for actual, expected in zip(shared(_array(values, backend)), (values + 2, np.sum((values + 2) ** 2), values + 1)):
+        _result(actual, expected, rtol=3e-5, atol=3e-5)
 
 
 # ---- fuse (reference tests/test_fusion.py) ---------------------------------------------
