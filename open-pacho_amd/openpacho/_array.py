@@ -18,7 +18,7 @@ import numpy as np
 from numpy.lib.mixins import NDArrayOperatorsMixin
 
 from ._ops import UFUNCS as _UFUNCS
-from ._ops import resolve_elementwise
+from ._ops import HostScalar, resolve_elementwise
 from .backends import get_backend
 from .exceptions import BackendMismatchError
 
@@ -249,24 +249,19 @@ def _common_backend(values):
 
 
 def _elementwise(ufunc, *inputs):
-    from ._fusion import Expression, trace_op
-
     if any(isinstance(v, Expression) for v in inputs):
         return trace_op(ufunc, *inputs)
-    from ._ops import HostScalar
-
     backend = _common_backend(inputs)
-    resolved, _ = resolve_elementwise(ufunc, inputs)
+    resolved, shape = resolve_elementwise(ufunc, inputs)
     for dtype in resolved:
         backend.validate_dtype(dtype)
     by_value = backend.name in _NATIVE_SCALAR_BACKENDS
     operands = []
     for value, dtype in zip(inputs, resolved):
-        if by_value and np.isscalar(value):
+        if by_value and not isinstance(value, ndarray) and np.isscalar(value):
             operands.append(HostScalar(value, dtype))
         else:
             operands.append(asarray(value, dtype=dtype, backend=backend))
-    shape = np.broadcast_shapes(*(v.shape for v in operands))
     data = backend.elementwise(ufunc.__name__, operands, shape, resolved[-1])
     return ndarray._wrap(data, shape, resolved[-1], backend)
 
@@ -473,6 +468,24 @@ def mean(a, axis=None, dtype=None, out=None, keepdims=False):
 
 def matmul(a, b, *, padding=False):
     """Matrix product; ``padding`` is an opt-in hint for the GPU GEMM kernels."""
+    if (
+        padding is False
+        and type(a) is ndarray
+        and type(b) is ndarray
+        and a._backend is b._backend
+        and a._dtype == b._dtype
+        and 0 < len(a._shape) <= 2
+        and 0 < len(b._shape) <= 2
+    ):
+        # Same backend and dtype, no batch axes: the general path below would
+        # convert nothing and broadcast nothing; skip straight to the product.
+        backend, dtype = a._backend, a._dtype
+        if a._shape[-1] != b._shape[0]:
+            raise ValueError("matmul inner dimensions do not match")
+        if dtype.kind == "b":
+            raise NotImplementedError("Boolean matmul is not supported")
+        shape = a._shape[:-1] + b._shape[1:]
+        return ndarray._wrap(backend.matmul(a, b, shape, dtype), shape, dtype, backend)
     if padding is not False:
         from ._padding import validate_padding
 
@@ -516,3 +529,7 @@ for _fn in (sum, amin, amax, mean, reshape, transpose, dot, diag, zeros_like, on
     _FUNCTIONS[getattr(np, _fn.__name__)] = _fn
 _FUNCTIONS[np.min] = amin
 _FUNCTIONS[np.max] = amax
+
+# Imported last: _fusion builds on ndarray (import cycle), and a function-level
+# import would run on every eager elementwise call.
+from ._fusion import Expression, trace_op  # noqa: E402

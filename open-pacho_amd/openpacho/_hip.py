@@ -18,7 +18,6 @@ failing call raises.
 
 import ctypes
 from collections import OrderedDict
-from contextlib import contextmanager
 from math import prod
 from threading import RLock
 from weakref import WeakSet
@@ -108,6 +107,30 @@ def _collapse(shape, strides):
     return tuple(m[0] for m in merged), tuple(m[1] for m in merged)
 
 
+class _Active:
+    """The backend lock, refused once the backend is closed.
+
+    A plain context manager: entering it costs a lock acquire, where a
+    generator-based one costs a generator per operation on the dispatch path.
+    """
+
+    __slots__ = ("_backend",)
+
+    def __init__(self, backend):
+        self._backend = backend
+
+    def __enter__(self):
+        backend = self._backend
+        backend._lock.acquire()
+        if backend._closed:
+            backend._lock.release()
+            raise RuntimeError("hip backend is closed")
+
+    def __exit__(self, *exc):
+        self._backend._lock.release()
+        return False
+
+
 class HIPBackend:
     name = "hip"
     blas = "custom"
@@ -118,6 +141,7 @@ class HIPBackend:
     def __init__(self, device=None):
         self._lib = lib_.load()
         self._lock = RLock()
+        self._guard = _Active(self)
         self._leases = WeakSet()
         self._kernels = OrderedDict()
         self._ctx = None
@@ -144,12 +168,8 @@ class HIPBackend:
         status = getattr(self._lib, name)(self._ctx, *args)
         lib_.check(self._lib, status, name)
 
-    @contextmanager
     def _active(self):
-        with self._lock:
-            if self._closed:
-                raise RuntimeError("hip backend is closed")
-            yield
+        return self._guard
 
     def execution_scope(self):
         """Hold the backend lock for one plan execution."""
@@ -186,6 +206,8 @@ class HIPBackend:
     # ---- protocol: dtypes, storage, transfers --------------------------------------
 
     def validate_dtype(self, dtype):
+        if isinstance(dtype, np.dtype) and dtype in lib_.DTYPE_CODES:
+            return dtype  # already a supported, native-order dtype
         dtype = check_dtype(dtype)
         if dtype not in lib_.DTYPE_CODES:
             raise UnsupportedDtypeError(f"hip backend does not support {dtype}")

@@ -14,6 +14,7 @@ Mapped reductions use the extrema contract of the reduction kernels
 (NaN propagates, min prefers -0, max prefers +0).
 """
 
+from functools import lru_cache
 from math import prod
 
 import numpy as np
@@ -363,10 +364,17 @@ class HIPLowering:
 
 def eager_source(name, args, shape, dtype):
     """Source of one eager elementwise operation (a one-node fused group)."""
-    leaves = [_Leaf(getattr(a, "_host_scalar", False), a.dtype, a.shape) for a in args]
-    dtype = np.dtype(dtype)
-    resolved = tuple(np.dtype(a.dtype) for a in args)
+    operands = tuple((bool(getattr(a, "_host_scalar", False)), np.dtype(a.dtype), tuple(a.shape)) for a in args)
+    return _eager_source(name, operands, tuple(shape), np.dtype(dtype))
+
+
+@lru_cache(maxsize=1024)
+def _eager_source(name, operands, shape, dtype):
+    # Keyed by what the source depends on (operation, operand kinds, dtypes
+    # and shapes): repeated eager operations skip the code generation.
+    leaves = [_Leaf(scalar, leaf_dtype, leaf_shape) for scalar, leaf_dtype, leaf_shape in operands]
+    resolved = tuple(leaf_dtype for _, leaf_dtype, _ in operands)
     if name == "cast":
         resolved = (resolved[0],)
-    nodes = [(name, list(range(len(args))), resolved, dtype)]
-    return elementwise_source(tuple(shape), leaves, nodes, dtype)
+    nodes = [(name, list(range(len(operands))), resolved, dtype)]
+    return elementwise_source(shape, leaves, nodes, dtype)

@@ -6,6 +6,8 @@ resolution is delegated to ``ufunc.resolve_dtypes``, and integer ``power`` is
 rejected. ``where`` resolves its branches with ``np.result_type``.
 """
 
+from functools import lru_cache
+
 import numpy as np
 
 _NAMES = (
@@ -72,12 +74,29 @@ def _operand_shape(value):
     return np.shape(value)
 
 
+def broadcast_shape(shapes):
+    """np.broadcast_shapes, with the common all-equal case answered directly."""
+    shapes = [tuple(shape) for shape in shapes if shape != ()]  # scalars broadcast to anything
+    if not shapes:
+        return ()
+    if all(shape == shapes[0] for shape in shapes[1:]):
+        return shapes[0]
+    return np.broadcast_shapes(*shapes)
+
+
+@lru_cache(maxsize=4096)
+def _resolved_dtypes(ufunc, types):
+    # NumPy's loop resolution depends only on the operand types (dtypes, or
+    # Python scalar types under weak promotion), so it is memoized by them.
+    return tuple(np.dtype(d) for d in ufunc.resolve_dtypes(types + (None,)))
+
+
 def resolve_elementwise(ufunc, inputs):
     """Return ``(resolved dtypes, broadcast shape)`` for one elementwise call.
 
     ``resolved`` lists the operand dtypes followed by the output dtype.
     """
-    shape = np.broadcast_shapes(*(_operand_shape(v) for v in inputs))
+    shape = broadcast_shape([_operand_shape(v) for v in inputs])
     if ufunc is np.where:
         samples = []
         for value in inputs[1:]:
@@ -91,7 +110,7 @@ def resolve_elementwise(ufunc, inputs):
         return (np.dtype(bool), branch, branch, branch), shape
     if ufunc not in UFUNCS.values():
         raise NotImplementedError(f"Unsupported elementwise operation {ufunc.__name__}")
-    resolved = ufunc.resolve_dtypes(tuple(_operand_type(v) for v in inputs) + (None,))
+    resolved = _resolved_dtypes(ufunc, tuple(_operand_type(v) for v in inputs))
     if ufunc is np.power and resolved[-1].kind in "iu":
         raise NotImplementedError("Integer power is not supported; cast to float or multiply explicitly")
-    return tuple(np.dtype(d) for d in resolved), shape
+    return resolved, shape
