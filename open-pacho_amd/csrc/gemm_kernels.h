@@ -44,6 +44,7 @@
 #pragma once
 
 #include <algorithm>
+#include <type_traits>
 
 #include "gemm.h"
 
@@ -239,6 +240,76 @@ constexpr int WM = 128, WN = 64;
 // distinct banks (measured: removes the LDS bank conflicts of padded rows).
 __device__ __forceinline__ int swizzle(int row) { return (row >> 1) & 3; }
 
+// An operand whose K axis is strided in memory (B stored [k][n], or A stored
+// [k][m] when transposed) is read as 16-byte vectors along its tile rows:
+// each thread loads a 2 (k) x 4 (row) block, k = 2 kh + {0, 1} (kh = t % 8),
+// rows 4 b .. 4 b + 3 (b = t / 8), two global_load_dwordx4 instead of eight
+// scalar loads, and writes it transposed, 8 bytes per row, into LDS rows of
+// 16 k values padded to PS floats. The 80-byte row stride keeps both these
+// writes (32 lanes: 4 row blocks x 8 k pairs) and the fragment reads (16
+// consecutive rows) on distinct banks. Measured on one box: 8192^3 85.6% ->
+// 89.0% of peak, 4096^3 83.8% -> 88.1%.
+constexpr int PS = 20;
+
+template <int MODE>
+struct PairLoader {
+  static_assert(kThreads == 512 && BM == 256 && BN == 256, "8 k pairs x 64 row blocks of 4 per slice");
+  hpd::f32x4 v[2];
+  int kh, b;
+
+  __device__ __forceinline__ void init(int tid) {
+    kh = tid & 7;
+    b = tid >> 3;
+  }
+
+  // Same contract as SliceLoader::load with KM = true: element (r, k) at
+  // p[k * ld + r]; rows past `rows` read clamped addresses (their outputs are
+  // never stored); in mode 2, k at or past kp reads as +0.
+  __device__ __forceinline__ void load(const float* p, int64_t r0, int64_t rows, int64_t ld, int64_t kp,
+                                       int64_t k0) {
+    const int64_t c = r0 + 4 * b;
+#pragma unroll
+    for (int r = 0; r < 2; ++r) {
+      const int64_t k = k0 + 2 * kh + r;
+      if (MODE == 2 && k >= kp) {
+        v[r] = hpd::f32x4{0.f, 0.f, 0.f, 0.f};
+        continue;
+      }
+      const float* q = p + k * ld;
+      if (MODE == 0 || c + 3 < rows) {
+        v[r] = *reinterpret_cast<const f32x4u*>(q + c);
+      } else {
+#pragma unroll
+        for (int e = 0; e < 4; ++e) v[r][e] = q[c + e < rows ? c + e : rows - 1];
+      }
+    }
+  }
+
+  __device__ __forceinline__ void store(float* buf) const {
+    typedef float f32x2 __attribute__((ext_vector_type(2)));
+#pragma unroll
+    for (int e = 0; e < 4; ++e) *reinterpret_cast<f32x2*>(buf + (4 * b + e) * PS + 2 * kh) = f32x2{v[0][e], v[1][e]};
+  }
+
+  __device__ __forceinline__ static int64_t origin(int64_t s0, int64_t ld) { return s0 * 16 * ld; }
+};
+
+// LDS row stride of an operand and its loader: k-contiguous operands use the
+// swizzled 16-float rows of SliceLoader, K-strided ones the padded pair rows.
+template <bool KM>
+constexpr int lds_stride() {
+  return KM ? PS : S;
+}
+template <bool KM, int MODE, int ROWS>
+using Loader = typename std::conditional<KM, PairLoader<MODE>, SliceLoader<float, ROWS, false, MODE, kThreads>>::type;
+
+// Fragment read offset of lane `lane` for tile row `row0 + (lane & 15)`.
+template <bool KM>
+__device__ __forceinline__ int fragment_offset(int row0, int lane) {
+  const int row = row0 + (lane & 15);
+  return KM ? row * PS + 4 * (lane >> 4) : row * S + 4 * ((lane >> 4) ^ swizzle(lane & 15));
+}
+
 // Eight waves in a 2x4 grid of 128x64 wave tiles. Accumulator layout: lane
 // holds column lane%16, rows 4*(lane/16) + r.
 struct Layout {
@@ -249,7 +320,7 @@ struct Layout {
   static __device__ __forceinline__ int col(int wave, int j, int lane) { return (wave & 3) * WN + 16 * j + (lane & 15); }
 };
 
-// One workgroup per compute unit (64 KB of LDS, 2 waves per SIMD). The
+// One workgroup per compute unit (64-72 KB of LDS, 2 waves per SIMD). The
 // pipeline per K slice s:
 //   - global loads of slice s+2 into registers, issued first;
 //   - 128 MFMAs per wave on the fragments of slice s, already in registers;
@@ -267,26 +338,26 @@ template <int MODE, bool STREAM_K, bool TA, bool TB>
 __global__ __launch_bounds__(kThreads, 1) void kernel(const float* __restrict__ A, const float* __restrict__ B,
                                                       float* __restrict__ C, int64_t M, int64_t N, int64_t K,
                                                       BatchDesc bd, TileMap tmap, Split sp) {
-  __shared__ __attribute__((aligned(16))) float As[2][BM * S];
-  __shared__ __attribute__((aligned(16))) float Bs[2][BN * S];
+  constexpr int SA = lds_stride<TA>(), SB = lds_stride<!TB>();
+  __shared__ __attribute__((aligned(16))) float As[2][BM * SA];
+  __shared__ __attribute__((aligned(16))) float Bs[2][BN * SB];
 
   const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
   const int wm = wave >> 2, wn = wave & 3;
 
   // Global -> register -> LDS operand slices. A is k-contiguous ([m][k])
   // unless TA ([k][m]); B is row-contiguous ([k][n]) unless TB ([n][k]).
-  // Untransposed: A as 2 float4 per thread (rows tid/4 + 128i, k quad
-  // tid%4), B as 8 scalars per thread (column tid%256, k quads
-  // 2*(tid/256) + {0, 1}; 64 lanes read 256 contiguous bytes of one B row).
-  SliceLoader<float, BM, TA, MODE, kThreads> la;
-  SliceLoader<float, BN, !TB, MODE, kThreads> lb;
+  // k-contiguous operands load 2 float4 groups per thread (rows tid/4 +
+  // 128i, k quad tid%4); K-strided ones 2 float4 row vectors (PairLoader).
+  Loader<TA, MODE, BM> la;
+  Loader<!TB, MODE, BN> lb;
   la.init(tid);
   lb.init(tid);
   const int64_t lda = TA ? M : K, ldb = TB ? K : N;
   // Rows read by a lane differ by multiples of 16, so the swizzle of every
   // row it reads equals that of (lane & 15).
-  const int a_read = (wm * WM + (lane & 15)) * S + 4 * ((lane >> 4) ^ swizzle(lane & 15));
-  const int b_read = (wn * WN + (lane & 15)) * S + 4 * ((lane >> 4) ^ swizzle(lane & 15));
+  const int a_read = fragment_offset<TA>(wm * WM, lane);
+  const int b_read = fragment_offset<!TB>(wn * WN, lane);
 
   // Tile `tile` over K slices [s0, s1). slot < 0: the piece is the whole K
   // range and is stored to C; else it goes to workspace slot `slot`.
@@ -325,9 +396,9 @@ __global__ __launch_bounds__(kThreads, 1) void kernel(const float* __restrict__ 
     __syncthreads();
     hpd::f32x4 a[FM], b[FN], b_next[FN];
 #pragma unroll
-    for (int i = 0; i < FM; ++i) a[i] = *reinterpret_cast<const hpd::f32x4*>(&As[0][a_read + 16 * i * S]);
+    for (int i = 0; i < FM; ++i) a[i] = *reinterpret_cast<const hpd::f32x4*>(&As[0][a_read + 16 * i * SA]);
 #pragma unroll
-    for (int j = 0; j < FN; ++j) b[j] = *reinterpret_cast<const hpd::f32x4*>(&Bs[0][b_read + 16 * j * S]);
+    for (int j = 0; j < FN; ++j) b[j] = *reinterpret_cast<const hpd::f32x4*>(&Bs[0][b_read + 16 * j * SB]);
     __syncthreads();  // every wave has read buffer 0 before slice 0 refills it
     // Fragment read addresses of the next slice, carried across iterations:
     // indexing As[(s + 1) & 1] directly lets the compiler rematerialize the
@@ -346,8 +417,8 @@ __global__ __launch_bounds__(kThreads, 1) void kernel(const float* __restrict__ 
           for (int j = 0; j < FN; ++j)
             acc[i][j] = __builtin_amdgcn_mfma_f32_16x16x4f32(a[i][q], b[j][q], acc[i][j], 0, 0, 0);
         if (more) {
-          a[i] = *reinterpret_cast<const hpd::f32x4*>(a_src + 16 * i * S);
-          if (i >= FM - FN) b_next[i - (FM - FN)] = *reinterpret_cast<const hpd::f32x4*>(b_src + 16 * (i - (FM - FN)) * S);
+          a[i] = *reinterpret_cast<const hpd::f32x4*>(a_src + 16 * i * SA);
+          if (i >= FM - FN) b_next[i - (FM - FN)] = *reinterpret_cast<const hpd::f32x4*>(b_src + 16 * (i - (FM - FN)) * SB);
         }
         if (i == 5 && s + 2 < slices) store_slice(int(s & 1));
       }
