@@ -162,6 +162,74 @@ def cpu_gemm_baseline(p, gemm):
     }
 
 
+def vendor_gemm():
+    """The vendor BLAS on the headline shapes, for comparison only.
+
+    Runs ``bench.py --vendor-child`` as a child process: PyTorch's ROCm build
+    brings its own HIP runtime, which finds no GPU in a process that has
+    already loaded the hip backend's library (built against /opt/rocm). Never
+    feeds ``value``.
+    """
+    import subprocess
+
+    try:
+        child = subprocess.run(
+            [sys.executable, os.path.abspath(__file__), "--vendor-child"],
+            capture_output=True, text=True, timeout=240,
+        )
+    except subprocess.TimeoutExpired:
+        log("vendor: child timed out; skipped")
+        return {}
+    if child.returncode != 0 or not child.stdout.strip():
+        log(f"vendor: child exited {child.returncode}: {child.stderr.strip()[-300:]}")
+        return {}
+    return json.loads(child.stdout.strip().splitlines()[-1])
+
+
+def vendor_gemm_child():
+    """PyTorch's fp32/fp64 matmul on ROCm (hipBLASLt or rocBLAS; full fp32,
+    TF32 off) on 8192^3 / 4096^3, timed with events on torch's stream."""
+    try:
+        import torch
+    except ImportError as error:
+        log(f"vendor: torch not importable ({error}); skipped")
+        return {}
+    if not torch.cuda.is_available():
+        log("vendor: torch sees no GPU; skipped")
+        return {}
+    torch.backends.cuda.matmul.allow_tf32 = False
+    out = {}
+    for name, n, dtype, peak in (
+        ("vendor_gemm_f32_8192", 8192, torch.float32, PEAK_FP32_TFLOPS),
+        ("vendor_gemm_f64_4096", 4096, torch.float64, PEAK_FP64_TFLOPS),
+    ):
+        generator = torch.Generator(device="cuda").manual_seed(3)
+        a = torch.rand((n, n), device="cuda", dtype=dtype, generator=generator) * 2 - 1
+        b = torch.rand((n, n), device="cuda", dtype=dtype, generator=generator) * 2 - 1
+        for _ in range(3):
+            torch.matmul(a, b)
+        torch.cuda.synchronize()
+        start, stop = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+        reps = 10
+        start.record()
+        for _ in range(reps):
+            c = torch.matmul(a, b)
+        stop.record()
+        torch.cuda.synchronize()
+        ms = start.elapsed_time(stop) / reps
+        tflops = 2.0 * n**3 / (ms * 1e-3) / 1e12
+        out[name] = {
+            "value": round(tflops * 1e3, 1),
+            "unit": "GFLOP/s",
+            "kernel_ms": round(ms, 4),
+            "frac_of_peak": round(tflops / peak, 4),
+            "library": "torch.matmul on ROCm (hipBLASLt/rocBLAS), full precision",
+        }
+        del a, b, c
+        torch.cuda.empty_cache()
+    return out
+
+
 def bench_extras(p, hip, only, skip_cpu):
     from oracle import numpy_backend
 
@@ -314,6 +382,8 @@ def bench_extras(p, hip, only, skip_cpu):
             "steps": [s["kind"] for s in mlp.explain(x, *params)["steps"]],
             "roofline": roofline("mfma", flops, ms),
         }
+    if want("vendor"):
+        extra.update(vendor_gemm())
     return extra
 
 
@@ -323,8 +393,12 @@ def main(argv=None):
     parser.add_argument("--steps", type=int, default=10)
     parser.add_argument("--warmup", type=int, default=3)
     parser.add_argument("--skip-cpu", action="store_true", help="omit the CPU baselines")
-    parser.add_argument("--only", default="", help="comma-separated extras to run (gemv,norm,rng,gemm_f64,gemm_padded,gemm_batched,mlp; copy = PMC calibration, only when named); 'none' for the headline only")
+    parser.add_argument("--vendor-child", action="store_true", help=argparse.SUPPRESS)
+    parser.add_argument("--only", default="", help="comma-separated extras to run (gemv,norm,rng,gemm_f64,gemm_padded,gemm_batched,mlp,vendor; copy = PMC calibration, only when named); 'none' for the headline only")
     args = parser.parse_args(argv)
+    if args.vendor_child:
+        print(json.dumps(vendor_gemm_child()), flush=True)
+        return 0
     if args.gpus != 1:
         print(
             f"bench.py measures one MI355X: this build has no multi-GPU path (asked for --gpus {args.gpus}). "
@@ -346,6 +420,9 @@ def main(argv=None):
     del gemm["a"], gemm["b"]
     only = set() if not args.only else {s.strip() for s in args.only.split(",") if s.strip()}
     extra = {} if only == {"none"} else bench_extras(p, hip, only, args.skip_cpu)
+    vendor = extra.get("vendor_gemm_f32_8192")
+    if vendor:
+        vendor["hip_over_vendor"] = round(vendor["kernel_ms"] / gemm["kernel_ms"], 4)
     for name, entry in extra.items():
         log(f"{name}: {entry['value']} {entry['unit']}" + (f" ({entry['roofline']['frac']:.1%} of roofline)" if "roofline" in entry else ""))
     result = {

@@ -88,6 +88,16 @@ __device__ __forceinline__ void logical_tile(int64_t t, const TileMap& tm, int64
   tj = r / gm;
 }
 
+// Origin of the tile computed for the tile owning [t0, t0 + tile) of an
+// axis of `extent`. Edge tiles move back to end at the extent, so every row
+// they read is in bounds and the interior loaders serve them; their first
+// t0 - origin rows belong to the previous tile and are not stored. Only an
+// axis shorter than one tile keeps origin 0 and reads clamped rows.
+__device__ __forceinline__ int64_t tile_origin(int64_t t0, int64_t extent, int tile) {
+  const int64_t last = extent > tile ? extent - tile : 0;
+  return t0 < last ? t0 : last;
+}
+
 // Consecutive ids of a count-long range, renumbered so that ids landing on one
 // XCD (ids i % 8) get a contiguous block of the range.
 __device__ __forceinline__ int64_t xcd_major(int64_t id, int64_t count) {
@@ -181,36 +191,46 @@ struct SliceLoader {
   }
 
   // p: operand origin at this piece's first k; r0: first tile row; rows:
-  // operand rows; ld: leading dimension; kp: valid k from the origin.
+  // operand rows; ld: leading dimension; kp: valid k from the origin. In
+  // mode 2 only the slice holding the K edge, or a tile that an operand
+  // shorter than one tile leaves partly empty, takes the checked path; the
+  // test is uniform over the workgroup, so other slices load as in mode 0.
   __device__ __forceinline__ void load(const T* p, int64_t r0, int64_t rows, int64_t ld, int64_t kp, int64_t k0) {
+    if (MODE == 2 && (k0 + 16 > kp || r0 + ROWS > rows)) {
+      load_checked(p, r0, rows, ld, kp, k0);
+      return;
+    }
     if (!KM) {
-      if (MODE == 2 && k0 + 16 > kp) {
-#pragma unroll
-        for (int i = 0; i < NV; ++i) {
-          const int64_t r = r0 + row0 + (THREADS / G) * i;
-          const T* q = p + (r < rows ? r : rows - 1) * ld;
-#pragma unroll
-          for (int e = 0; e < W; ++e) reg[i][e] = k0 + kbase + e < kp ? q[k0 + kbase + e] : T(0);
-        }
-        return;
-      }
 #pragma unroll
       for (int i = 0; i < NV; ++i) {
         const int64_t r = r0 + row0 + (THREADS / G) * i;
-        reg[i] = *reinterpret_cast<const VL*>(p + (MODE == 0 || r < rows ? r : rows - 1) * ld + k0 + kbase);
+        reg[i] = *reinterpret_cast<const VL*>(p + r * ld + k0 + kbase);
       }
     } else {
-      const int64_t r = MODE == 0 || r0 + row0 < rows ? r0 + row0 : rows - 1;
-      if (MODE == 2 && k0 + 16 > kp) {
 #pragma unroll
-        for (int e = 0; e < NE; ++e) {
-          const int64_t k = k0 + kbase + e;
-          reg[e / W][e % W] = k < kp ? p[k * ld + r] : T(0);
-        }
-        return;
+      for (int e = 0; e < NE; ++e) reg[e / W][e % W] = p[(k0 + kbase + e) * ld + r0 + row0];
+    }
+  }
+
+  // Rows past `rows` read clamped addresses (their outputs are never
+  // stored); k at or past kp reads as +0.
+  __device__ __forceinline__ void load_checked(const T* p, int64_t r0, int64_t rows, int64_t ld, int64_t kp,
+                                               int64_t k0) {
+    if (!KM) {
+#pragma unroll
+      for (int i = 0; i < NV; ++i) {
+        const int64_t r = r0 + row0 + (THREADS / G) * i;
+        const T* q = p + (r < rows ? r : rows - 1) * ld;
+#pragma unroll
+        for (int e = 0; e < W; ++e) reg[i][e] = k0 + kbase + e < kp ? q[k0 + kbase + e] : T(0);
       }
+    } else {
+      const int64_t r = r0 + row0 < rows ? r0 + row0 : rows - 1;
 #pragma unroll
-      for (int e = 0; e < NE; ++e) reg[e / W][e % W] = p[(k0 + kbase + e) * ld + r];
+      for (int e = 0; e < NE; ++e) {
+        const int64_t k = k0 + kbase + e;
+        reg[e / W][e % W] = k < kp ? p[k * ld + r] : T(0);
+      }
     }
   }
 
@@ -263,26 +283,27 @@ struct PairLoader {
   }
 
   // Same contract as SliceLoader::load with KM = true: element (r, k) at
-  // p[k * ld + r]; rows past `rows` read clamped addresses (their outputs are
-  // never stored); in mode 2, k at or past kp reads as +0.
+  // p[k * ld + r]; in mode 2 the K-edge slice and tiles of operands shorter
+  // than one tile take a checked path (uniform test): rows past `rows` read
+  // clamped addresses (outputs never stored), k at or past kp reads as +0.
   __device__ __forceinline__ void load(const float* p, int64_t r0, int64_t rows, int64_t ld, int64_t kp,
                                        int64_t k0) {
     const int64_t c = r0 + 4 * b;
+    if (MODE == 2 && (k0 + 16 > kp || r0 + BN > rows)) {
 #pragma unroll
-    for (int r = 0; r < 2; ++r) {
-      const int64_t k = k0 + 2 * kh + r;
-      if (MODE == 2 && k >= kp) {
-        v[r] = hpd::f32x4{0.f, 0.f, 0.f, 0.f};
-        continue;
-      }
-      const float* q = p + k * ld;
-      if (MODE == 0 || c + 3 < rows) {
-        v[r] = *reinterpret_cast<const f32x4u*>(q + c);
-      } else {
+      for (int r = 0; r < 2; ++r) {
+        const int64_t k = k0 + 2 * kh + r;
+        const float* q = p + (k < kp ? k : kp - 1) * ld;
 #pragma unroll
-        for (int e = 0; e < 4; ++e) v[r][e] = q[c + e < rows ? c + e : rows - 1];
+        for (int e = 0; e < 4; ++e) {
+          const float x = q[c + e < rows ? c + e : rows - 1];
+          v[r][e] = k < kp ? x : 0.f;
+        }
       }
+      return;
     }
+#pragma unroll
+    for (int r = 0; r < 2; ++r) v[r] = *reinterpret_cast<const f32x4u*>(p + (k0 + 2 * kh + r) * ld + c);
   }
 
   __device__ __forceinline__ void store(float* buf) const {
@@ -291,8 +312,68 @@ struct PairLoader {
     for (int e = 0; e < 4; ++e) *reinterpret_cast<f32x2*>(buf + (4 * b + e) * PS + 2 * kh) = f32x2{v[0][e], v[1][e]};
   }
 
+  // Pipeline interface: issue the global loads of a slice, commit it to LDS.
+  __device__ __forceinline__ void issue(const float* p, int64_t r0, int64_t rows, int64_t ld, int64_t kp, int64_t k0,
+                                        float*) {
+    load(p, r0, rows, ld, kp, k0);
+  }
+  __device__ __forceinline__ void commit(float* buf) const { store(buf); }
+  static constexpr bool kDirect = false;
+
   __device__ __forceinline__ static int64_t origin(int64_t s0, int64_t ld) { return s0 * 16 * ld; }
 };
+
+// A k-contiguous operand in modes 0 and 1, rows 16-byte aligned (host
+// check): its K slice goes from global memory straight into LDS with
+// global_load_lds_dwordx4, without registers or ds_write. LDS-DMA writes
+// 16 bytes per lane at consecutive addresses, so wave w fills 16-row chunks
+// 2w and 2w + 1 (1 KB each) and lane l fetches the global group that the
+// swizzle places at its position: row 16c + l / 4, k group (l % 4) ^
+// swizzle(row). Completion is tracked by vmcnt; kernels wait for vmcnt(0)
+// before the barrier that publishes a slice. Every row read is in bounds.
+template <int MODE>
+struct DmaLoader {
+  static_assert(MODE == 0, "in-bounds rows only: mode 1 moves edge tiles inside, mode 2 stages");
+  static_assert(kThreads == 512 && BM == 256 && BN == 256, "16 chunks of 16 rows per slice");
+  int chunk0, lane;
+
+  __device__ __forceinline__ void init(int tid) {
+    chunk0 = 2 * __builtin_amdgcn_readfirstlane(tid >> 6);
+    lane = tid & 63;
+  }
+
+  __device__ __forceinline__ void issue(const float* p, int64_t r0, int64_t rows, int64_t ld, int64_t, int64_t k0,
+                                        float* buf) const {
+#pragma unroll
+    for (int i = 0; i < 2; ++i) {
+      const int c = chunk0 + i;
+      const int row = 16 * c + (lane >> 2);
+      const float* src = p + (r0 + row) * ld + k0 + 4 * ((lane & 3) ^ swizzle(row));
+      // The LDS operand is an address-space-3 pointer: a C cast converts it.
+      __builtin_amdgcn_global_load_lds(static_cast<const void*>(src),
+                                       (__attribute__((address_space(3))) void*)(buf + 256 * c), 16, 0, 0);
+    }
+  }
+  __device__ __forceinline__ void commit(float*) const {}
+  static constexpr bool kDirect = true;
+
+  __device__ __forceinline__ static int64_t origin(int64_t s0, int64_t) { return s0 * 16; }
+};
+
+// Register-staged k-contiguous loads (mode 2: the K-edge slice zero-fills).
+template <int MODE>
+struct StagedLoader : SliceLoader<float, 256, false, MODE, kThreads> {
+  __device__ __forceinline__ void issue(const float* p, int64_t r0, int64_t rows, int64_t ld, int64_t kp, int64_t k0,
+                                        float*) {
+    this->load(p, r0, rows, ld, kp, k0);
+  }
+  __device__ __forceinline__ void commit(float* buf) const { this->store(buf); }
+  static constexpr bool kDirect = false;
+};
+
+// s_waitcnt vmcnt(0) (gfx9 encoding: vmcnt in bits 3:0 and 15:14, expcnt
+// 6:4, lgkmcnt 11:8 left at their maxima).
+constexpr unsigned kWaitVmcnt0 = 0x0F70;
 
 // LDS row stride of an operand and its loader: k-contiguous operands use the
 // swizzled 16-float rows of SliceLoader, K-strided ones the padded pair rows.
@@ -300,8 +381,12 @@ template <bool KM>
 constexpr int lds_stride() {
   return KM ? PS : S;
 }
-template <bool KM, int MODE, int ROWS>
-using Loader = typename std::conditional<KM, PairLoader<MODE>, SliceLoader<float, ROWS, false, MODE, kThreads>>::type;
+// Modes 0 and 1 share the interior loaders: mode 1 (M, N >= one tile) moves
+// edge tiles inside the operands instead of clamping their rows.
+template <bool KM, int MODE>
+using Loader = typename std::conditional<
+    KM, PairLoader<MODE == 1 ? 0 : MODE>,
+    typename std::conditional<MODE == 2, StagedLoader<MODE>, DmaLoader<MODE == 1 ? 0 : MODE>>::type>::type;
 
 // Fragment read offset of lane `lane` for tile row `row0 + (lane & 15)`.
 template <bool KM>
@@ -347,10 +432,11 @@ __global__ __launch_bounds__(kThreads, 1) void kernel(const float* __restrict__ 
 
   // Global -> register -> LDS operand slices. A is k-contiguous ([m][k])
   // unless TA ([k][m]); B is row-contiguous ([k][n]) unless TB ([n][k]).
-  // k-contiguous operands load 2 float4 groups per thread (rows tid/4 +
-  // 128i, k quad tid%4); K-strided ones 2 float4 row vectors (PairLoader).
-  Loader<TA, MODE, BM> la;
-  Loader<!TB, MODE, BN> lb;
+  // k-contiguous operands go straight to LDS (DmaLoader; register-staged in
+  // mode 2), K-strided ones as 2 float4 row vectors per thread (PairLoader).
+  Loader<TA, MODE> la;
+  Loader<!TB, MODE> lb;
+  constexpr bool kDirect = decltype(la)::kDirect || decltype(lb)::kDirect;
   la.init(tid);
   lb.init(tid);
   const int64_t lda = TA ? M : K, ldb = TB ? K : N;
@@ -366,19 +452,34 @@ __global__ __launch_bounds__(kThreads, 1) void kernel(const float* __restrict__ 
     logical_tile(tile, tmap, batch, ti, tj);
     int64_t a_off, b_off;
     batch_offsets(batch, bd, a_off, b_off);
+    // Owned tile [m0, m0 + BM) x [n0, n0 + BN), computed at (ms, ns).
     const int64_t m0 = ti * BM, n0 = tj * BN;
+    const int64_t ms = MODE == 0 ? m0 : tile_origin(m0, M, BM), ns = MODE == 0 ? n0 : tile_origin(n0, N, BN);
     // Operand origins at the piece's first k; kp = valid k extent from there.
     const float* Ap = A + a_off + decltype(la)::origin(s0, lda);
     const float* Bp = B + b_off + decltype(lb)::origin(s0, ldb);
     const int64_t kp = K - s0 * BK;
     const int64_t slices = s1 - s0;
-    auto load_slice = [&](int64_t k0) {
-      la.load(Ap, m0, M, lda, kp, k0);
-      lb.load(Bp, n0, N, ldb, kp, k0);
+    // Slice k0 into LDS buffer `buf`: issue() starts the global reads (direct
+    // loads land in LDS by themselves), commit() writes staged registers.
+    // Direct loads go first. The compiler waits for vmcnt(0) before any
+    // ds_write while an LDS-DMA is in flight (it cannot tell the buffers
+    // apart), so the staged commit waits for them anyway; issued first they
+    // have the most time. Same-box A/B at 8192^3: direct first 89.8-90.1% of
+    // peak, staged first 84.6%, no direct loads 88.6-89.2%.
+    auto load_slice = [&](int64_t k0, int buf) {
+      if (decltype(la)::kDirect) la.issue(Ap, ms, M, lda, kp, k0, As[buf]);
+      if (decltype(lb)::kDirect) lb.issue(Bp, ns, N, ldb, kp, k0, Bs[buf]);
+      if (!decltype(la)::kDirect) la.issue(Ap, ms, M, lda, kp, k0, As[buf]);
+      if (!decltype(lb)::kDirect) lb.issue(Bp, ns, N, ldb, kp, k0, Bs[buf]);
     };
     auto store_slice = [&](int buf) {
-      la.store(As[buf]);
-      lb.store(Bs[buf]);
+      la.commit(As[buf]);
+      lb.commit(Bs[buf]);
+    };
+    auto publish = [&] {
+      if (kDirect) __builtin_amdgcn_s_waitcnt(kWaitVmcnt0);
+      __syncthreads();
     };
 
     hpd::f32x4 acc[FM][FN];
@@ -387,13 +488,13 @@ __global__ __launch_bounds__(kThreads, 1) void kernel(const float* __restrict__ 
 #pragma unroll
       for (int j = 0; j < FN; ++j) acc[i][j] = hpd::f32x4{0.f, 0.f, 0.f, 0.f};
 
-    load_slice(0);
+    load_slice(0, 0);
     store_slice(0);
     if (slices > 1) {
-      load_slice(BK);
+      load_slice(BK, 1);
       store_slice(1);
     }
-    __syncthreads();
+    publish();
     hpd::f32x4 a[FM], b[FN], b_next[FN];
 #pragma unroll
     for (int i = 0; i < FM; ++i) a[i] = *reinterpret_cast<const hpd::f32x4*>(&As[0][a_read + 16 * i * SA]);
@@ -408,7 +509,7 @@ __global__ __launch_bounds__(kThreads, 1) void kernel(const float* __restrict__ 
     const float* b_src = &Bs[1][b_read];
     for (int64_t s = 0; s < slices; ++s) {
       const bool more = s + 1 < slices;
-      if (s + 2 < slices) load_slice((s + 2) * BK);
+      if (s + 2 < slices) load_slice((s + 2) * BK, int(s & 1));
 #pragma unroll
       for (int i = 0; i < FM; ++i) {
 #pragma unroll
@@ -426,7 +527,7 @@ __global__ __launch_bounds__(kThreads, 1) void kernel(const float* __restrict__ 
       for (int j = 0; j < FN; ++j) b[j] = b_next[j];
       a_src = (s & 1) ? &As[1][a_read] : &As[0][a_read];
       b_src = (s & 1) ? &Bs[1][b_read] : &Bs[0][b_read];
-      __syncthreads();
+      publish();
     }
 
     if (slot < 0) {
@@ -435,11 +536,11 @@ __global__ __launch_bounds__(kThreads, 1) void kernel(const float* __restrict__ 
       for (int i = 0; i < FM; ++i) {
 #pragma unroll
         for (int j = 0; j < FN; ++j) {
-          const int64_t col = n0 + Layout::col(wave, j, lane);
+          const int64_t col = ns + Layout::col(wave, j, lane);
 #pragma unroll
           for (int r = 0; r < 4; ++r) {
-            const int64_t row = m0 + Layout::row(wave, i, lane, r);
-            if (MODE == 0 || (row < M && col < N)) Cb[row * N + col] = acc[i][j][r];
+            const int64_t row = ms + Layout::row(wave, i, lane, r);
+            if (MODE == 0 || (row >= m0 && row < M && col >= n0 && col < N)) Cb[row * N + col] = acc[i][j][r];
           }
         }
       }
@@ -525,8 +626,9 @@ __global__ __launch_bounds__(kThreads, 1) void kernel(const double* __restrict__
   // thread (rows tid/8 + 64i, k pair tid%8), B as 4 scalars per thread
   // (column tid%128, k rows 4*(tid/128) + {0..3}; 64 lanes read 512
   // contiguous bytes of one B row), stored as 2 pairs.
-  SliceLoader<double, BM, TA, MODE, kThreads> la;
-  SliceLoader<double, BN, !TB, MODE, kThreads> lb;
+  // Mode 1 moves edge tiles inside the operands: interior loads.
+  SliceLoader<double, BM, TA, MODE == 1 ? 0 : MODE, kThreads> la;
+  SliceLoader<double, BN, !TB, MODE == 1 ? 0 : MODE, kThreads> lb;
   la.init(tid);
   lb.init(tid);
   const int64_t lda = TA ? M : K, ldb = TB ? K : N;
@@ -543,13 +645,14 @@ __global__ __launch_bounds__(kThreads, 1) void kernel(const double* __restrict__
     int64_t a_off, b_off;
     batch_offsets(batch, bd, a_off, b_off);
     const int64_t m0 = ti * BM, n0 = tj * BN;
+    const int64_t ms = MODE == 0 ? m0 : tile_origin(m0, M, BM), ns = MODE == 0 ? n0 : tile_origin(n0, N, BN);
     const double* Ap = A + a_off + decltype(la)::origin(s0, lda);
     const double* Bp = B + b_off + decltype(lb)::origin(s0, ldb);
     const int64_t kp = K - s0 * BK;
     const int64_t slices = s1 - s0;
     auto load_slice = [&](int64_t k0) {
-      la.load(Ap, m0, M, lda, kp, k0);
-      lb.load(Bp, n0, N, ldb, kp, k0);
+      la.load(Ap, ms, M, lda, kp, k0);
+      lb.load(Bp, ns, N, ldb, kp, k0);
     };
     auto store_slice = [&](int buf) {
       la.store(As[buf]);
@@ -617,11 +720,11 @@ __global__ __launch_bounds__(kThreads, 1) void kernel(const double* __restrict__
       for (int i = 0; i < FM; ++i) {
 #pragma unroll
         for (int j = 0; j < FN; ++j) {
-          const int64_t col = n0 + Layout::col(wave, j, lane);
+          const int64_t col = ns + Layout::col(wave, j, lane);
 #pragma unroll
           for (int r = 0; r < 4; ++r) {
-            const int64_t row = m0 + Layout::row(wave, i, lane, r);
-            if (MODE == 0 || (row < M && col < N)) Cb[row * N + col] = acc[i][j][r];
+            const int64_t row = ms + Layout::row(wave, i, lane, r);
+            if (MODE == 0 || (row >= m0 && row < M && col >= n0 && col < N)) Cb[row * N + col] = acc[i][j][r];
           }
         }
       }
@@ -678,11 +781,13 @@ __global__ __launch_bounds__(256) void fixup_kernel(T* __restrict__ C, int64_t M
   int64_t batch, ti, tj;
   logical_tile(sp.dp_tiles + tl, tmap, batch, ti, tj);
   T* Cb = C + batch * M * N;
-  const int64_t col = tj * BN + L::col(wave, j, lane);
+  // The tile was computed at its (possibly moved) origin, as in the kernels.
+  const int64_t m0 = ti * BM, n0 = tj * BN;
+  const int64_t col = tile_origin(n0, N, BN) + L::col(wave, j, lane);
 #pragma unroll
   for (int r = 0; r < 4; ++r) {
-    const int64_t row = ti * BM + L::row(wave, i, lane, r);
-    if (row < M && col < N) Cb[row * N + col] = sum[r];
+    const int64_t row = tile_origin(m0, M, BM) + L::row(wave, i, lane, r);
+    if (row >= m0 && row < M && col >= n0 && col < N) Cb[row * N + col] = sum[r];
   }
 }
 
@@ -755,8 +860,10 @@ void launch_split(hp_ctx* ctx, Whole whole, Cut cut, Fix fixup, int threads, con
 }
 
 // Mode of a product: 0 interior, 1 M/N edges, 2 any K (see the kernels).
+// 0: whole tiles; 1: K whole, edge tiles moved inside M, N >= one tile;
+// 2: a K edge (zero fill) or an axis shorter than a tile (clamped rows).
 int mode_of(int64_t m, int64_t n, int64_t k, int64_t bm, int64_t bn, int64_t bk) {
-  if (k % bk != 0) return 2;
+  if (k % bk != 0 || m < bm || n < bn) return 2;
   return m % bm == 0 && n % bn == 0 ? 0 : 1;
 }
 
@@ -767,7 +874,14 @@ void run_f32(hp_ctx* ctx, const float* a, const float* b, float* c, int64_t m, i
   TileMap tm;
   prepare(m, n, batch, BM, BN, tm);
   auto fix = fixup_kernel<float, hpd::f32x4, Layout>;
-  switch (mode_of(m, n, k, BM, BN, BK)) {
+  int mode = mode_of(m, n, k, BM, BN, BK);
+  // Modes 0 and 1 load the k-contiguous operands (A unless TA, B if TB)
+  // straight into LDS, which needs 16-byte aligned rows. K % 16 == 0 there,
+  // so the base pointers decide; mode 2's register-staged loads serve views
+  // at other element offsets.
+  const bool aligned = (TA || reinterpret_cast<uintptr_t>(a) % 16 == 0) && (!TB || reinterpret_cast<uintptr_t>(b) % 16 == 0);
+  if (!aligned) mode = 2;
+  switch (mode) {
     case 0:
       launch_split<float, BM, BN>(ctx, kernel<0, false, TA, TB>, kernel<0, true, TA, TB>, fix, kThreads, a, b, c, m,
                                   n, k, bd, tm, BK, "gemm_f32");

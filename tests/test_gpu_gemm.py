@@ -115,7 +115,8 @@ def test_batched_broadcast_products(hip, dtype, shapes):
         (300, 200, 100),  # K edge with K % 4 == 0
         (1, 1, 1),
         (31, 33, 4099),  # long K, partial tiles
-        (640, 384, 48),
+        (640, 384, 48),  # M/N edges with K whole: edge tiles moved inside
+        (777, 300, 64),  # moved edge tiles that own 9 rows / 44 columns
     ],
 )
 def test_kernel_modes_against_float64(hip, dtype, m, n, k):
@@ -139,6 +140,7 @@ STREAM_K_CASES = [
     (np.float32, (), 1000, 700, 2000),  # M/N edges, 12 tiles
     (np.float32, (), 777, 555, 1111),  # K odd
     (np.float32, (3,), 300, 200, 700),  # batched: 6 tiles
+    (np.float32, (2,), 600, 300, 512),  # batched, moved edge tiles summed by the fixup
     (np.float64, (), 1000, 1000, 2000),  # 32 tiles over 256 workers, extra > 0
     (np.float64, (2,), 256, 384, 1024),  # interior fp64, batched
     (np.float64, (), 129, 65, 3001),  # K odd, fp64
@@ -338,7 +340,7 @@ def test_padding_preserves_special_values_and_signed_zero(hip):
 # ---- products of private transposes (hp_gemm_layout), reference
 # tests/test_clblast.py:410-440 and tests/test_compiled_layout.py:43-80
 
-LAYOUT_SHAPES = [(35, 33, 39), (300, 257, 129), (512, 1024, 768), (700, 2001, 517)]  # m, k, n
+LAYOUT_SHAPES = [(35, 33, 39), (300, 257, 129), (512, 1024, 768), (700, 2001, 517), (700, 1024, 517)]  # m, k, n
 
 
 @pytest.mark.parametrize("dtype", [np.float32, np.float64])
