@@ -127,3 +127,21 @@ def test_config3_row_norms_full_size(hip):
     ref_rel = np.abs(ref - oracle[sample]) / oracle[sample]
     assert np.sqrt(np.mean(rel[sample] ** 2)) <= 2 * np.sqrt(np.mean(ref_rel**2)) + 1e-9
     assert rel.max() < 1e-6
+
+
+@pytest.mark.parametrize("dtype", [np.float32, np.float64])
+def test_flat_norm_single_pass_repeats_across_grid_sizes(hip, dtype):
+    # The single-row kernel's last workgroup merges every workgroup's pair
+    # and resets the completion counter: calls of different grid sizes in a
+    # row must each see a fresh count, and repeats are bitwise identical.
+    rng = np.random.default_rng(17)
+    sizes = [1 << 22, 5000, 3 * 4096 + 1, 1 << 20, 2, (1 << 24) + 7]
+    hosts = [rng.uniform(-1, 1, n).astype(dtype) for n in sizes]
+    arrays = [p.asarray(h, backend=hip) for h in hosts]
+    first = [p.asnumpy(p.linalg.norm(a)) for a in arrays]
+    for _ in range(2):
+        for a, want, host in zip(arrays, first, hosts):
+            got = p.asnumpy(p.linalg.norm(a))
+            assert got.tobytes() == want.tobytes()
+            exact_norm = np.sqrt(np.sum(host.astype(np.float64) ** 2))
+            assert abs(float(got) - exact_norm) <= 4 * np.finfo(dtype).eps * exact_norm
