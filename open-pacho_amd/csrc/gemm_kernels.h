@@ -410,8 +410,9 @@ struct Layout {
 //   - global loads of slice s+2 into registers, issued first;
 //   - 128 MFMAs per wave on the fragments of slice s, already in registers;
 //     after the 16 MFMAs of A fragment i, that register is refilled with
-//     fragment i of slice s+1 from LDS (B fragments are double-buffered), so
-//     LDS reads overlap the matrix pipe instead of stalling each slice start;
+//     fragment i of slice s+1 from LDS (B fragments are double-buffered and
+//     refilled after A fragments 0-3), so LDS reads overlap the matrix pipe
+//     instead of stalling each slice start;
 //   - after the MFMAs of fragment 5, slice s+2 goes from registers to the LDS
 //     buffer that held slice s (all waves read it during slice s-1);
 //   - one barrier.
@@ -519,7 +520,9 @@ __global__ __launch_bounds__(kThreads, 1) void kernel(const float* __restrict__ 
             acc[i][j] = __builtin_amdgcn_mfma_f32_16x16x4f32(a[i][q], b[j][q], acc[i][j], 0, 0, 0);
         if (more) {
           a[i] = *reinterpret_cast<const hpd::f32x4*>(a_src + 16 * i * SA);
-          if (i >= FM - FN) b_next[i - (FM - FN)] = *reinterpret_cast<const hpd::f32x4*>(b_src + 16 * (i - (FM - FN)) * SB);
+          // B refills ride on the first FN A fragments, so only A refills
+          // are in flight at the barrier (same-box A/B: +0.3-0.6% of peak).
+          if (i < FN) b_next[i] = *reinterpret_cast<const hpd::f32x4*>(b_src + 16 * i * SB);
         }
         if (i == 5 && s + 2 < slices) store_slice(int(s & 1));
       }
