@@ -128,7 +128,7 @@ class ExecutionPlan:
         self.padding = validate_padding(padding)
         factory = getattr(backend, "create_lowering", None)
         self.lowering = None if factory is None else factory()
-        self._scope = getattr(backend, "execution_scope", None)
+        self._execution_scope = getattr(backend, "execution_scope", None)
         self.nodes = _post_order(outputs)
         # A consumer that reads a node twice (x*x) counts once.
         self.uses = Counter(child for node in self.nodes for child in {id(c) for c in node.inputs})
@@ -142,7 +142,7 @@ class ExecutionPlan:
             for _, kind, _, payload in self.steps
         )
         if launches < getattr(backend, "execution_scope_min_steps", 0):
-            self._scope = None
+            self._execution_scope = None
         self.live_uses = Counter(id(a) for _, _, args, _ in self.steps for a in args)
         self.live_uses.update(id(o) for o in outputs)
 
@@ -251,8 +251,8 @@ class ExecutionPlan:
     # ---- execution ----------------------------------------------------------------
 
     def execute(self, bindings):
-        if self._scope is not None:
-            with self._scope():
+        if self._execution_scope is not None:
+            with self._execution_scope():
                 return self._run(bindings)
         return self._run(bindings)
 

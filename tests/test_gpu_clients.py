@@ -127,3 +127,23 @@ def test_conjugate_gradient_on_resident_operands(hip, dtype, tolerance):
     np.testing.assert_allclose(p.asnumpy(x), exact, rtol=50 * tolerance, atol=50 * tolerance)
     true_residual = host_b.astype(np.float64) - host_a.astype(np.float64) @ p.asnumpy(x).astype(np.float64)
     assert np.linalg.norm(true_residual) / np.linalg.norm(host_b) < 10 * tolerance
+
+
+def test_solver_downloads_only_scalar_diagnostics(hip, monkeypatch):
+    # Reference tests/test_residency.py:30-46: during the solve only the
+    # one-element convergence diagnostics cross to the host.
+    A = p.asarray([[4.0, 1.0], [1.0, 3.0]], dtype=p.float32, backend=hip)
+    b = p.asarray([1.0, 2.0], dtype=p.float32, backend=hip)
+    original = hip.download
+    sizes = []
+
+    def track_download(a):
+        sizes.append(a.size)
+        assert a.size == 1, "Solver transferred a vector or matrix during iteration"
+        return original(a)
+
+    with monkeypatch.context() as patch:
+        patch.setattr(hip, "download", track_download)
+        x, iterations = _conjugate_gradient(A, b, 1e-6, 50)
+    assert sizes and iterations < 50
+    np.testing.assert_allclose(p.asnumpy(x), [1 / 11, 7 / 11], rtol=1e-5)
