@@ -44,12 +44,17 @@ void enter(hp_ctx* ctx) {
   set_device(ctx->device);
 }
 
+// Each block leaves the cache as soon as its free succeeds, so a failure part
+// way through leaves only blocks that are still allocated: a freed pointer is
+// never handed out again (reference test_cuda_lifetime.py:79-126).
 static void release_cache_locked(hp_ctx* ctx) {
   if (ctx->free_blocks.empty()) return;
   HP_CHECK(hipStreamSynchronize(ctx->stream));
-  for (auto& entry : ctx->free_blocks) HP_CHECK(hipFree(entry.second));
-  ctx->free_blocks.clear();
-  ctx->cached_bytes = 0;
+  for (auto it = ctx->free_blocks.begin(); it != ctx->free_blocks.end();) {
+    HP_CHECK(hipFree(it->second));
+    ctx->cached_bytes -= it->first;
+    it = ctx->free_blocks.erase(it);
+  }
 }
 
 static void* pool_alloc(hp_ctx* ctx, size_t bytes) {
