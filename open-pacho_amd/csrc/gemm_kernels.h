@@ -273,6 +273,7 @@ constexpr int PS = 20;
 
 template <int MODE>
 struct PairLoader {
+  static_assert(MODE != 1, "mode 1 moves edge tiles inside the operands and uses the interior loader");
   static_assert(kThreads == 512 && BM == 256 && BN == 256, "8 k pairs x 64 row blocks of 4 per slice");
   hpd::f32x4 v[2];
   int kh, b;
