@@ -159,6 +159,7 @@ class HIPBackend:
         if status:
             raise BackendUnavailableError(f"HIP initialization failed: {lib_.last_error(self._lib)}")
         self._ctx = ctx
+        self._pool_limit = self.device_info.memory_bytes // 4  # hp_init's default
 
     # ---- plumbing ---------------------------------------------------------------
 
@@ -258,6 +259,22 @@ class HIPBackend:
     def release_cached_memory(self):
         with self._active():
             self._call("hp_release_cached")
+
+    @property
+    def pool_limit(self):
+        """Bytes of freed blocks the pool keeps for reuse (a quarter of device
+        memory by default). Blocks larger than the limit are freed at once;
+        lowering it frees cached blocks until the cache fits."""
+        return self._pool_limit
+
+    @pool_limit.setter
+    def pool_limit(self, value):
+        value = int(value)
+        if value < 0:
+            raise ValueError("pool limit must be non-negative")
+        with self._active():
+            self._call("hp_set_pool_limit", value)
+        self._pool_limit = value
 
     def pool_stats(self):
         values = [ctypes.c_int64(0) for _ in range(4)]

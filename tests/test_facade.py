@@ -497,3 +497,27 @@ def test_non_full_transpose_gather_is_not_folded():
         product = trace.matmul(gather, right, (shape[0], 9), np.float32)
         plan = ExecutionPlan(backend, (product,), False)
         assert [s[1] for s in plan.steps] == ["gather", "matmul"]
+
+
+def test_import_and_numpy_backend_load_nothing_native():
+    # Reference tests/test_cuda.py:682-704: importing the package and using
+    # the NumPy backend must not load the optional device runtimes.
+    import subprocess
+    import sys
+    import textwrap
+
+    package = Path(p.__file__).resolve().parents[1]
+    script = textwrap.dedent(
+        f"""
+        import sys
+        sys.path.insert(0, {str(package)!r})
+        import openpacho
+        assert openpacho.get_backend("numpy").name == "numpy"
+        maps = open("/proc/self/maps").read()
+        for library in ("libpacho_hip", "libamdhip64", "libhiprtc"):
+            assert library not in maps, library + " loaded without the hip backend"
+        assert "openpacho._hip_lib" not in sys.modules and "torch" not in sys.modules
+        """
+    )
+    completed = subprocess.run([sys.executable, "-c", script], capture_output=True, text=True, timeout=120)
+    assert completed.returncode == 0, completed.stderr or completed.stdout

@@ -285,3 +285,36 @@ def test_close_is_idempotent_and_invalidates_arrays():
         p.asnumpy(live)
     with pytest.raises(RuntimeError):
         live + 1.0
+
+
+def test_pool_respects_byte_limit(hip):
+    # Reference tests/test_cuda.py:598-612: freed blocks stay cached only
+    # within the pool's byte limit.
+    previous = hip.pool_limit
+    try:
+        hip.release_cached_memory()
+        hip.pool_limit = 1024
+        for _ in range(12):
+            temporary = p.empty((128,), dtype=np.float32, backend=hip)
+            del temporary
+        gc.collect()
+        hip.synchronize()
+        stats = hip.pool_stats()
+        assert stats["cached_bytes"] <= hip.pool_limit and stats["cached_items"] <= 128
+        large = p.full(4096, 2.0, dtype=np.float32, backend=hip)  # above the limit: freed, not cached
+        del large
+        gc.collect()
+        assert hip.pool_stats()["cached_bytes"] <= 1024
+        with pytest.raises(ValueError):
+            hip.pool_limit = -1
+    finally:
+        hip.pool_limit = previous
+        hip.release_cached_memory()
+
+
+def test_bool_fill_rebinds_without_changing_previous_output(hip):
+    # Reference tests/test_cuda.py:530-534.
+    first = p.full(33, True, dtype=np.bool_, backend=hip)
+    second = p.full(33, False, dtype=np.bool_, backend=hip)
+    np.testing.assert_array_equal(p.asnumpy(first), np.ones(33, dtype=np.bool_))
+    np.testing.assert_array_equal(p.asnumpy(second), np.zeros(33, dtype=np.bool_))
