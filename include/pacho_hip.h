@@ -144,7 +144,10 @@ int hp_pad_copy(hp_ctx* ctx, int elem_bytes, const void* src, void* dst, int64_t
 /* ---- dense linear algebra ------------------------------------------------ */
 
 /* C[b] = A[b'] @ B[b''] for row-major A (m x k), B (k x n), C (m x n),
- * dtype HP_F32 or HP_F64, on MFMA. The output batch is contiguous with
+ * dtype HP_F32 or HP_F64 on MFMA; the integer dtypes (wrapping modulo
+ * 2^bits) and HP_BOOL (or of ands) on a tiled integer kernel, as the
+ * reference OpenCL backend's generic product (_opencl.py:386-420); vector
+ * operands are 1-row / 1-column matrices. The output batch is contiguous with
  * batch_rank dims `batch_shape`; operand batch offsets are
  * sum_d idx_d * a_batch_strides[d] (resp. b_...) elements, 0 = broadcast.
  * batch_rank <= 6. k == 0 writes zeros. C is never read.

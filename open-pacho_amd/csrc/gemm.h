@@ -17,6 +17,21 @@ struct BatchDesc {
   int64_t b_stride[6];
 };
 
+// Element offsets of batch `batch`'s A and B matrices (row-major batch index).
+__device__ __forceinline__ void batch_offsets(int64_t batch, const BatchDesc& bd, int64_t& a_off, int64_t& b_off) {
+  a_off = 0;
+  b_off = 0;
+  int64_t rest = batch;
+  for (int d = bd.rank - 1; d >= 0; --d) {
+    const int64_t extent = bd.shape[d];
+    const int64_t q = rest / extent;
+    const int64_t idx = rest - q * extent;
+    rest = q;
+    a_off += idx * bd.a_stride[d];
+    b_off += idx * bd.b_stride[d];
+  }
+}
+
 // C[b] = op(A[b']) @ op(B[b'']) for b < batch, m x n x k, row-major; op(A)
 // is A stored [k][m] for layout t?, op(B) is B stored [n][k] for ?t.
 using Run = void (*)(hp_ctx* ctx, const void* a, const void* b, void* c, int64_t m, int64_t n, int64_t k,

@@ -114,19 +114,7 @@ __device__ __forceinline__ int64_t sk_worker(const Split& sp, int64_t g) {
   return g < long_runs ? g / (sp.base + 1) : sp.extra + (g - long_runs) / sp.base;
 }
 
-__device__ __forceinline__ void batch_offsets(int64_t batch, const BatchDesc& bd, int64_t& a_off, int64_t& b_off) {
-  a_off = 0;
-  b_off = 0;
-  int64_t rest = batch;
-  for (int d = bd.rank - 1; d >= 0; --d) {
-    const int64_t extent = bd.shape[d];
-    const int64_t q = rest / extent;
-    const int64_t idx = rest - q * extent;
-    rest = q;
-    a_off += idx * bd.a_stride[d];
-    b_off += idx * bd.b_stride[d];
-  }
-}
+using hpgemm::batch_offsets;
 
 // ---------------------------------------------------------------- loaders ----
 

@@ -371,12 +371,19 @@ class HIPBackend:
 
     def matmul(self, a, b, shape, dtype):
         dtype = np.dtype(dtype)
-        if dtype.kind != "f":
-            raise NotImplementedError("hip matmul requires float32 or float64")
         code = lib_.DTYPE_CODES[dtype]
         k = a.shape[-1]
         out = self.empty(shape, dtype)
         if not prod(shape):
+            return out
+        if dtype.kind != "f":
+            # Integer and bool products (hp_gemm's integer kernel): vectors are
+            # 1-row / 1-column matrices of the same storage.
+            m = 1 if a.ndim == 1 else a.shape[-2]
+            n = 1 if b.ndim == 1 else b.shape[-1]
+            a_batch = a.shape[:-2] if a.ndim > 1 else ()
+            b_batch = b.shape[:-2] if b.ndim > 1 else ()
+            self._gemm(code, a, b, out, m, n, k, np.broadcast_shapes(a_batch, b_batch), a_batch, b_batch)
             return out
         if b.ndim == 1:
             with self._active():
@@ -390,7 +397,10 @@ class HIPBackend:
         n = b.shape[-1]
         batch = tuple(shape[: len(shape) - (1 if a.ndim == 1 else 2)])
         a_batch = a.shape[:-2] if a.ndim > 1 else ()
-        b_batch = b.shape[:-2]
+        self._gemm(code, a, b, out, m, n, k, batch, a_batch, b.shape[:-2])
+        return out
+
+    def _gemm(self, code, a, b, out, m, n, k, batch, a_batch, b_batch):
         dims, a_strides, b_strides = self._batch_strides(batch, a_batch, m * k, b_batch, k * n)
         with self._active():
             self._call(
@@ -405,7 +415,6 @@ class HIPBackend:
                 lib_.int64_array(a_strides),
                 lib_.int64_array(b_strides),
             )
-        return out
 
     @staticmethod
     def _ptrs(*arrays):

@@ -419,3 +419,57 @@ def test_special_values_and_subnormals_propagate(hip, dtype):
     finite = ~np.isnan(want)
     np.testing.assert_array_equal(got[finite], want[finite])
     assert got[2, 1] == tiny and got[2, 2] == -tiny  # subnormals are not flushed
+
+
+INTEGER_SHAPES = [
+    ((37, 129), (129,)),  # reference tests/test_matrix_optimization.py:33-40 shapes
+    ((1, 4097), (4097,)),
+    ((3, 1025), (1025,)),
+    ((1, 4096), (4096,)),
+    ((4097,), (4097,)),
+    ((7,), (7, 5)),
+    ((33, 70), (70, 45)),
+    ((2, 1, 5, 7), (3, 7, 4)),
+    ((4, 0), (0, 3)),
+]
+
+
+@pytest.mark.parametrize("dtype", [np.int32, np.int64, np.uint32, np.uint64])
+@pytest.mark.parametrize("shapes", INTEGER_SHAPES)
+def test_integer_products_wrap_like_numpy_bit_for_bit(hip, dtype, shapes):
+    # Integer products sum in the operand type modulo 2^bits (NumPy and the
+    # reference OpenCL backend's generic product): small values check the
+    # indexing, full-range values the wraparound.
+    rng = np.random.default_rng(48)
+    info = np.iinfo(dtype)
+    for low, high in ((-3, 4), (info.min, info.max)):
+        low = max(low, info.min)
+        a, b = (rng.integers(low, high, size=s, dtype=dtype, endpoint=True) for s in shapes)
+        with np.errstate(over="ignore"):
+            want = a @ b
+        got = p.asarray(a, backend=hip) @ p.asarray(b, backend=hip)
+        assert got.dtype == want.dtype and got.shape == want.shape
+        np.testing.assert_array_equal(p.asnumpy(got), want)
+
+
+def test_mixed_integer_promotion_and_compiled_product(hip):
+    a = np.arange(-6, 6, dtype=np.int32).reshape(3, 4)
+    b = np.arange(8, dtype=np.int64).reshape(4, 2) * (2**40)
+    A, B = p.asarray(a, backend=hip), p.asarray(b, backend=hip)
+    np.testing.assert_array_equal(p.asnumpy(A @ B), a @ b)
+    np.testing.assert_array_equal(p.asnumpy(p.compile(lambda x, y: x @ y + 1)(A, B)), a @ b + 1)
+    with pytest.raises(NotImplementedError, match="Boolean matmul"):
+        p.asarray(a > 0, backend=hip) @ p.asarray(b > 0, backend=hip)
+
+
+def test_bool_gemm_abi_is_or_of_ands(hip):
+    # The facade rejects bool products (reference _array.py:471); the C-ABI
+    # computes them as NumPy does: any(a[i, :] & b[:, j]).
+    rng = np.random.default_rng(7)
+    a = rng.random((19, 33)) < 0.05
+    b = rng.random((33, 21)) < 0.05
+    A, B = p.asarray(a, backend=hip), p.asarray(b, backend=hip)
+    out = p.empty((19, 21), dtype=np.bool_, backend=hip)
+    with hip._active():
+        hip._call("hp_gemm", 0, *hip._ptrs(A, B, out), 19, 21, 33, 0, None, None, None)
+    np.testing.assert_array_equal(p.asnumpy(out), a @ b)
