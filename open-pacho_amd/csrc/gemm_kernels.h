@@ -66,6 +66,7 @@ struct Split {
   int64_t base, extra;
   int64_t slices;  // K slices per tile
   void* partial;   // [workers][2][tile elements]: a worker's first and last cut piece
+  int moved;       // edge tiles were computed at tile_origin() (the fixup stores alike)
 };
 
 constexpr int64_t kGroupM = 8;
@@ -179,24 +180,46 @@ struct SliceLoader {
   }
 
   // p: operand origin at this piece's first k; r0: first tile row; rows:
-  // operand rows; ld: leading dimension; kp: valid k from the origin. In
-  // mode 2 only the slice holding the K edge, or a tile that an operand
-  // shorter than one tile leaves partly empty, takes the checked path; the
-  // test is uniform over the workgroup, so other slices load as in mode 0.
+  // operand rows; ld: leading dimension; kp: valid k from the origin. Rows
+  // past `rows` load clamped addresses (their outputs are never stored); in
+  // mode 2 the slice holding the K edge zero-fills past kp.
+  //
+  // fp32 (kUniformCheck): a workgroup-uniform test sends only the K-edge
+  // slice, or a tile that an operand shorter than one tile leaves partly
+  // empty, to the checked path, and other slices load without clamps
+  // (4097x2049x3001: 54.6% -> 58% of peak). The fp64 kernels run at the
+  // 256-VGPR limit, where that split spills (4096^2 x 4095: 76% -> 64%), so
+  // they clamp rows on every slice and check K in the K-edge slice.
+  static constexpr bool kUniformCheck = sizeof(T) == 4;
+
   __device__ __forceinline__ void load(const T* p, int64_t r0, int64_t rows, int64_t ld, int64_t kp, int64_t k0) {
-    if (MODE == 2 && (k0 + 16 > kp || r0 + ROWS > rows)) {
+    constexpr bool kClamp = MODE != 0 && !kUniformCheck;
+    if (kUniformCheck && MODE == 2 && (k0 + 16 > kp || r0 + ROWS > rows)) {
       load_checked(p, r0, rows, ld, kp, k0);
       return;
     }
     if (!KM) {
+      if (!kUniformCheck && MODE == 2 && k0 + 16 > kp) {
+        load_checked(p, r0, rows, ld, kp, k0);
+        return;
+      }
 #pragma unroll
       for (int i = 0; i < NV; ++i) {
         const int64_t r = r0 + row0 + (THREADS / G) * i;
-        reg[i] = *reinterpret_cast<const VL*>(p + r * ld + k0 + kbase);
+        reg[i] = *reinterpret_cast<const VL*>(p + (!kClamp || r < rows ? r : rows - 1) * ld + k0 + kbase);
       }
     } else {
+      const int64_t r = !kClamp || r0 + row0 < rows ? r0 + row0 : rows - 1;
+      if (!kUniformCheck && MODE == 2 && k0 + 16 > kp) {
 #pragma unroll
-      for (int e = 0; e < NE; ++e) reg[e / W][e % W] = p[(k0 + kbase + e) * ld + r0 + row0];
+        for (int e = 0; e < NE; ++e) {
+          const int64_t k = k0 + kbase + e;
+          reg[e / W][e % W] = k < kp ? p[k * ld + r] : T(0);
+        }
+        return;
+      }
+#pragma unroll
+      for (int e = 0; e < NE; ++e) reg[e / W][e % W] = p[(k0 + kbase + e) * ld + r];
     }
   }
 
@@ -637,7 +660,10 @@ __global__ __launch_bounds__(kThreads, 1) void kernel(const double* __restrict__
     int64_t a_off, b_off;
     batch_offsets(batch, bd, a_off, b_off);
     const int64_t m0 = ti * BM, n0 = tj * BN;
-    const int64_t ms = MODE == 0 ? m0 : tile_origin(m0, M, BM), ns = MODE == 0 ? n0 : tile_origin(n0, N, BN);
+    // Edge tiles move inside in mode 1 only: mode 2's clamped loads serve
+    // edges, and moving the origin there too costs these kernels (at the
+    // 256-VGPR limit) register spills.
+    const int64_t ms = MODE == 1 ? tile_origin(m0, M, BM) : m0, ns = MODE == 1 ? tile_origin(n0, N, BN) : n0;
     const double* Ap = A + a_off + decltype(la)::origin(s0, lda);
     const double* Bp = B + b_off + decltype(lb)::origin(s0, ldb);
     const int64_t kp = K - s0 * BK;
@@ -716,7 +742,8 @@ __global__ __launch_bounds__(kThreads, 1) void kernel(const double* __restrict__
 #pragma unroll
           for (int r = 0; r < 4; ++r) {
             const int64_t row = ms + Layout::row(wave, i, lane, r);
-            if (MODE == 0 || (row >= m0 && row < M && col >= n0 && col < N)) Cb[row * N + col] = acc[i][j][r];
+            const bool owned = MODE == 1 ? row >= m0 && col >= n0 : true;  // only mode 1 moves tiles
+            if (MODE == 0 || (owned && row < M && col < N)) Cb[row * N + col] = acc[i][j][r];
           }
         }
       }
@@ -775,10 +802,10 @@ __global__ __launch_bounds__(256) void fixup_kernel(T* __restrict__ C, int64_t M
   T* Cb = C + batch * M * N;
   // The tile was computed at its (possibly moved) origin, as in the kernels.
   const int64_t m0 = ti * BM, n0 = tj * BN;
-  const int64_t col = tile_origin(n0, N, BN) + L::col(wave, j, lane);
+  const int64_t col = (sp.moved ? tile_origin(n0, N, BN) : n0) + L::col(wave, j, lane);
 #pragma unroll
   for (int r = 0; r < 4; ++r) {
-    const int64_t row = tile_origin(m0, M, BM) + L::row(wave, i, lane, r);
+    const int64_t row = (sp.moved ? tile_origin(m0, M, BM) : m0) + L::row(wave, i, lane, r);
     if (row >= m0 && row < M && col >= n0 && col < N) Cb[row * N + col] = sum[r];
   }
 }
@@ -834,9 +861,10 @@ Split plan_split(int64_t total, int64_t slices, int64_t slots) {
 template <typename T, int BM, int BN, typename Whole, typename Cut, typename Fix>
 void launch_split(hp_ctx* ctx, Whole whole, Cut cut, Fix fixup, int threads, const T* a, const T* b, T* c,
                   int64_t m, int64_t n, int64_t k, const BatchDesc& bd, const TileMap& tm, int64_t bk,
-                  const char* name) {
+                  const char* name, bool moved) {
   const int per_cu = std::min(resident_per_cu(whole, threads), resident_per_cu(cut, threads));
   Split sp = plan_split(tm.total, hp::ceil_div(k, bk), int64_t(ctx->compute_units) * per_cu);
+  sp.moved = moved;
   if (sp.dp_tiles > 0) {
     whole<<<sp.dp_tiles, threads, 0, ctx->stream>>>(a, b, c, m, n, k, bd, tm, sp);
     hp::check_launch(name);
@@ -876,15 +904,15 @@ void run_f32(hp_ctx* ctx, const float* a, const float* b, float* c, int64_t m, i
   switch (mode) {
     case 0:
       launch_split<float, BM, BN>(ctx, kernel<0, false, TA, TB>, kernel<0, true, TA, TB>, fix, kThreads, a, b, c, m,
-                                  n, k, bd, tm, BK, "gemm_f32");
+                                  n, k, bd, tm, BK, "gemm_f32", false);
       break;
     case 1:
       launch_split<float, BM, BN>(ctx, kernel<1, false, TA, TB>, kernel<1, true, TA, TB>, fix, kThreads, a, b, c, m,
-                                  n, k, bd, tm, BK, "gemm_f32");
+                                  n, k, bd, tm, BK, "gemm_f32", true);
       break;
     default:
       launch_split<float, BM, BN>(ctx, kernel<2, false, TA, TB>, kernel<2, true, TA, TB>, fix, kThreads, a, b, c, m,
-                                  n, k, bd, tm, BK, "gemm_f32");
+                                  n, k, bd, tm, BK, "gemm_f32", true);
   }
 }
 
@@ -898,15 +926,15 @@ void run_f64(hp_ctx* ctx, const double* a, const double* b, double* c, int64_t m
   switch (mode_of(m, n, k, BM, BN, BK)) {
     case 0:
       launch_split<double, BM, BN>(ctx, kernel<0, false, TA, TB>, kernel<0, true, TA, TB>, fix, kThreads, a, b, c,
-                                   m, n, k, bd, tm, BK, "gemm_f64");
+                                   m, n, k, bd, tm, BK, "gemm_f64", false);
       break;
     case 1:
       launch_split<double, BM, BN>(ctx, kernel<1, false, TA, TB>, kernel<1, true, TA, TB>, fix, kThreads, a, b, c,
-                                   m, n, k, bd, tm, BK, "gemm_f64");
+                                   m, n, k, bd, tm, BK, "gemm_f64", true);
       break;
     default:
       launch_split<double, BM, BN>(ctx, kernel<2, false, TA, TB>, kernel<2, true, TA, TB>, fix, kThreads, a, b, c,
-                                   m, n, k, bd, tm, BK, "gemm_f64");
+                                   m, n, k, bd, tm, BK, "gemm_f64", false);
   }
 }
 
