@@ -641,9 +641,10 @@ __global__ __launch_bounds__(kThreads, 1) void kernel(const double* __restrict__
   // thread (rows tid/8 + 64i, k pair tid%8), B as 4 scalars per thread
   // (column tid%128, k rows 4*(tid/128) + {0..3}; 64 lanes read 512
   // contiguous bytes of one B row), stored as 2 pairs.
-  // Mode 1 moves edge tiles inside the operands: interior loads.
-  SliceLoader<double, BM, TA, MODE == 1 ? 0 : MODE, kThreads> la;
-  SliceLoader<double, BN, !TB, MODE == 1 ? 0 : MODE, kThreads> lb;
+  // Edge tiles stay at their own origin and load clamped rows (modes 1, 2):
+  // moving them inside, as the fp32 kernel does, measured no faster here.
+  SliceLoader<double, BM, TA, MODE, kThreads> la;
+  SliceLoader<double, BN, !TB, MODE, kThreads> lb;
   la.init(tid);
   lb.init(tid);
   const int64_t lda = TA ? M : K, ldb = TB ? K : N;
@@ -660,17 +661,13 @@ __global__ __launch_bounds__(kThreads, 1) void kernel(const double* __restrict__
     int64_t a_off, b_off;
     batch_offsets(batch, bd, a_off, b_off);
     const int64_t m0 = ti * BM, n0 = tj * BN;
-    // Edge tiles move inside in mode 1 only: mode 2's clamped loads serve
-    // edges, and moving the origin there too costs these kernels (at the
-    // 256-VGPR limit) register spills.
-    const int64_t ms = MODE == 1 ? tile_origin(m0, M, BM) : m0, ns = MODE == 1 ? tile_origin(n0, N, BN) : n0;
     const double* Ap = A + a_off + decltype(la)::origin(s0, lda);
     const double* Bp = B + b_off + decltype(lb)::origin(s0, ldb);
     const int64_t kp = K - s0 * BK;
     const int64_t slices = s1 - s0;
     auto load_slice = [&](int64_t k0) {
-      la.load(Ap, ms, M, lda, kp, k0);
-      lb.load(Bp, ns, N, ldb, kp, k0);
+      la.load(Ap, m0, M, lda, kp, k0);
+      lb.load(Bp, n0, N, ldb, kp, k0);
     };
     auto store_slice = [&](int buf) {
       la.store(As[buf]);
@@ -738,12 +735,11 @@ __global__ __launch_bounds__(kThreads, 1) void kernel(const double* __restrict__
       for (int i = 0; i < FM; ++i) {
 #pragma unroll
         for (int j = 0; j < FN; ++j) {
-          const int64_t col = ns + Layout::col(wave, j, lane);
+          const int64_t col = n0 + Layout::col(wave, j, lane);
 #pragma unroll
           for (int r = 0; r < 4; ++r) {
-            const int64_t row = ms + Layout::row(wave, i, lane, r);
-            const bool owned = MODE == 1 ? row >= m0 && col >= n0 : true;  // only mode 1 moves tiles
-            if (MODE == 0 || (owned && row < M && col < N)) Cb[row * N + col] = acc[i][j][r];
+            const int64_t row = m0 + Layout::row(wave, i, lane, r);
+            if (MODE == 0 || (row < M && col < N)) Cb[row * N + col] = acc[i][j][r];
           }
         }
       }
@@ -930,7 +926,7 @@ void run_f64(hp_ctx* ctx, const double* a, const double* b, double* c, int64_t m
       break;
     case 1:
       launch_split<double, BM, BN>(ctx, kernel<1, false, TA, TB>, kernel<1, true, TA, TB>, fix, kThreads, a, b, c,
-                                   m, n, k, bd, tm, BK, "gemm_f64", true);
+                                   m, n, k, bd, tm, BK, "gemm_f64", false);
       break;
     default:
       launch_split<double, BM, BN>(ctx, kernel<2, false, TA, TB>, kernel<2, true, TA, TB>, fix, kThreads, a, b, c,
