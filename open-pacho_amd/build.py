@@ -6,7 +6,9 @@ backend loads it. Run: python open-pacho_amd/build.py [--jobs N]
 """
 
 import argparse
+import json
 import os
+import re
 import shutil
 import subprocess
 import sys
@@ -48,18 +50,37 @@ def hipcc():
     return found
 
 
+REMARK = re.compile(r"remark:\s+(.+?): (\S+) \[-Rpass-analysis=kernel-resource-usage\]")
+
+
+def _resources(lines):
+    """Per-kernel register, scratch and occupancy figures from the compiler's
+    kernel-resource-usage remarks (device functions that are not kernels are
+    reported too and kept)."""
+    kernels, current = {}, None
+    for line in lines:
+        match = REMARK.search(line)
+        if not match:
+            continue
+        key, value = match.group(1).strip(), match.group(2)
+        if key == "Function Name":
+            current = kernels.setdefault(value, {})
+        elif current is not None:
+            current[key] = int(value) if value.isdigit() else value
+    return kernels
+
+
 def _compile(source):
     obj = BUILD / (source.stem + ".o")
-    command = [hipcc(), *FLAGS, "-c", str(source), "-o", str(obj)]
+    command = [hipcc(), *FLAGS, "-Rpass-analysis=kernel-resource-usage", "-c", str(source), "-o", str(obj)]
     result = subprocess.run(command, capture_output=True, text=True)
+    lines = (result.stdout + result.stderr).splitlines()
     # hipcc's host pass warns that it does not know the packed-fp32 feature.
-    noise = ("packed-fp32-ops", "is not a recognized feature for this target")
-    log = "\n".join(
-        line for line in (result.stdout + result.stderr).splitlines() if not any(n in line for n in noise)
-    ).strip()
+    noise = ("packed-fp32-ops", "is not a recognized feature for this target", "kernel-resource-usage")
+    log = "\n".join(line for line in lines if not any(n in line for n in noise)).strip()
     if result.returncode:
         raise RuntimeError(f"hipcc failed for {source.name}:\n{log}")
-    return obj, log
+    return obj, log, _resources(lines)
 
 
 def build(jobs=None, verbose=False):
@@ -70,12 +91,16 @@ def build(jobs=None, verbose=False):
     jobs = jobs or min(len(sources), os.cpu_count() or 4, 16)
     with ThreadPoolExecutor(max_workers=jobs) as pool:
         results = list(pool.map(_compile, sources))
-    for obj, log in results:
+    resources = {}
+    for obj, log, kernels in results:
         if log and verbose:
             print(f"[{obj.name}] {log}")
+        resources[obj.stem] = kernels
+    # Read by tests/test_build_resources.py (register spills, occupancy).
+    (BUILD / "resources.json").write_text(json.dumps(resources, indent=1, sort_keys=True) + "\n")
     tmp = LIBRARY.with_suffix(".so.tmp")
     command = [hipcc(), f"--offload-arch={ARCH}", "-shared", "-fPIC", "-o", str(tmp)]
-    command += [str(obj) for obj, _ in results] + ["-lhiprtc"]
+    command += [str(obj) for obj, _, _ in results] + ["-lhiprtc"]
     result = subprocess.run(command, capture_output=True, text=True)
     if result.returncode:
         raise RuntimeError(f"link failed:\n{result.stdout}{result.stderr}")
