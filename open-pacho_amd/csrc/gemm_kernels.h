@@ -254,6 +254,10 @@ struct SliceLoader {
   __device__ __forceinline__ static int64_t origin(int64_t s0, int64_t ld) { return KM ? s0 * 16 * ld : s0 * 16; }
 };
 
+// s_waitcnt vmcnt(0) (gfx9 encoding: vmcnt in bits 3:0 and 15:14, expcnt
+// 6:4, lgkmcnt 11:8 left at their maxima).
+constexpr unsigned kWaitVmcnt0 = 0x0F70;
+
 // ------------------------------------------------------------------ fp32 ----
 
 namespace f32 {
@@ -382,10 +386,6 @@ struct StagedLoader : SliceLoader<float, 256, false, MODE, kThreads> {
   __device__ __forceinline__ void commit(float* buf) const { this->store(buf); }
   static constexpr bool kDirect = false;
 };
-
-// s_waitcnt vmcnt(0) (gfx9 encoding: vmcnt in bits 3:0 and 15:14, expcnt
-// 6:4, lgkmcnt 11:8 left at their maxima).
-constexpr unsigned kWaitVmcnt0 = 0x0F70;
 
 // LDS row stride of an operand and its loader: k-contiguous operands use the
 // swizzled 16-float rows of SliceLoader, K-strided ones the padded pair rows.
@@ -620,6 +620,56 @@ struct Layout {
   static __device__ __forceinline__ int col(int wave, int j, int lane) { return (wave & 1) * WN + 16 * j + (lane & 15); }
 };
 
+// A k-contiguous fp64 operand in modes 0 and 1 (rows 16-byte aligned, host
+// check): its K slice goes from global memory straight into LDS with
+// global_load_lds_dwordx4, as in the fp32 kernel. One instruction fills a
+// 1 KB chunk of 8 rows; lane l writes row 8c + l / 8 at slot l % 8, so it
+// fetches the k pair that the swizzle stores there: (l % 8) ^ swizzle(row).
+// Rows past `rows` read clamped addresses (mode 1; outputs never stored).
+template <int ROWS, int MODE>
+struct DmaLoader64 {
+  static_assert(MODE != 2, "the K-edge slice needs zero fill: staged loads only");
+  static_assert(kThreads == 512 && ROWS % 64 == 0, "ROWS / 64 chunks of 8 rows per wave");
+  static constexpr int kChunks = ROWS / 64;  // per wave
+  int chunk0, lane;
+
+  __device__ __forceinline__ void init(int tid) {
+    chunk0 = kChunks * __builtin_amdgcn_readfirstlane(tid >> 6);
+    lane = tid & 63;
+  }
+
+  __device__ __forceinline__ void issue(const double* p, int64_t r0, int64_t rows, int64_t ld, int64_t, int64_t k0,
+                                        double* buf) const {
+#pragma unroll
+    for (int i = 0; i < kChunks; ++i) {
+      const int c = chunk0 + i;
+      const int row = 8 * c + (lane >> 3);
+      const int64_t r = MODE == 0 || r0 + row < rows ? r0 + row : rows - 1;
+      const double* src = p + r * ld + k0 + 2 * ((lane & 7) ^ swizzle(row));
+      // The LDS operand is an address-space-3 pointer: a C cast converts it.
+      __builtin_amdgcn_global_load_lds(static_cast<const void*>(src),
+                                       (__attribute__((address_space(3))) void*)(buf + 128 * c), 16, 0, 0);
+    }
+  }
+  __device__ __forceinline__ void commit(double*) const {}
+  static constexpr bool kDirect = true;
+  __device__ __forceinline__ static int64_t origin(int64_t s0, int64_t) { return s0 * 16; }
+};
+
+// Register-staged fp64 operand slices behind the same issue/commit interface.
+template <int ROWS, bool KM, int MODE>
+struct Staged64 : SliceLoader<double, ROWS, KM, MODE, kThreads> {
+  __device__ __forceinline__ void issue(const double* p, int64_t r0, int64_t rows, int64_t ld, int64_t kp,
+                                        int64_t k0, double*) {
+    this->load(p, r0, rows, ld, kp, k0);
+  }
+  __device__ __forceinline__ void commit(double* buf) const { this->store(buf); }
+  static constexpr bool kDirect = false;
+};
+
+template <int ROWS, bool KM, int MODE>
+using Loader = typename std::conditional<!KM && MODE != 2, DmaLoader64<ROWS, MODE>, Staged64<ROWS, KM, MODE>>::type;
+
 // One workgroup per compute unit, the pipeline of the fp32 kernel: per slice,
 // global loads of slice s+2 first; MFMAs of slice s in two k halves of 8,
 // each A fragment refilled from LDS with slice s+1 right after its MFMAs and
@@ -643,8 +693,9 @@ __global__ __launch_bounds__(kThreads, 1) void kernel(const double* __restrict__
   // contiguous bytes of one B row), stored as 2 pairs.
   // Edge tiles stay at their own origin and load clamped rows (modes 1, 2):
   // moving them inside, as the fp32 kernel does, measured no faster here.
-  SliceLoader<double, BM, TA, MODE, kThreads> la;
-  SliceLoader<double, BN, !TB, MODE, kThreads> lb;
+  Loader<BM, TA, MODE> la;
+  Loader<BN, !TB, MODE> lb;
+  constexpr bool kDirect = decltype(la)::kDirect || decltype(lb)::kDirect;
   la.init(tid);
   lb.init(tid);
   const int64_t lda = TA ? M : K, ldb = TB ? K : N;
@@ -665,13 +716,23 @@ __global__ __launch_bounds__(kThreads, 1) void kernel(const double* __restrict__
     const double* Bp = B + b_off + decltype(lb)::origin(s0, ldb);
     const int64_t kp = K - s0 * BK;
     const int64_t slices = s1 - s0;
-    auto load_slice = [&](int64_t k0) {
-      la.load(Ap, m0, M, lda, kp, k0);
-      lb.load(Bp, n0, N, ldb, kp, k0);
+    // Direct (LDS-DMA) loads first, as in the fp32 kernel. Staged loaders are
+    // called through SliceLoader::load itself: at the 256-VGPR limit of the
+    // all-staged mode-2 kernels, one more inlined wrapper level reshuffled
+    // registers into spills (transposed A: 23 -> 209 spilled VGPRs).
+    auto load_slice = [&](int64_t k0, int buf) {
+      if constexpr (decltype(la)::kDirect) la.issue(Ap, m0, M, lda, kp, k0, As[buf]);
+      if constexpr (decltype(lb)::kDirect) lb.issue(Bp, n0, N, ldb, kp, k0, Bs[buf]);
+      if constexpr (!decltype(la)::kDirect) la.load(Ap, m0, M, lda, kp, k0);
+      if constexpr (!decltype(lb)::kDirect) lb.load(Bp, n0, N, ldb, kp, k0);
     };
     auto store_slice = [&](int buf) {
-      la.store(As[buf]);
-      lb.store(Bs[buf]);
+      la.commit(As[buf]);
+      lb.commit(Bs[buf]);
+    };
+    auto publish = [&] {
+      if (kDirect) __builtin_amdgcn_s_waitcnt(kWaitVmcnt0);
+      __syncthreads();
     };
 
     f64x4 acc[FM][FN];
@@ -680,13 +741,13 @@ __global__ __launch_bounds__(kThreads, 1) void kernel(const double* __restrict__
 #pragma unroll
       for (int j = 0; j < FN; ++j) acc[i][j] = f64x4{0.0, 0.0, 0.0, 0.0};
 
-    load_slice(0);
+    load_slice(0, 0);
     store_slice(0);
     if (slices > 1) {
-      load_slice(BK);
+      load_slice(BK, 1);
       store_slice(1);
     }
-    __syncthreads();
+    publish();
     hpd::f64x2 a[2][FM], b[2][FN];
 #pragma unroll
     for (int i = 0; i < FM; ++i) {
@@ -704,7 +765,7 @@ __global__ __launch_bounds__(kThreads, 1) void kernel(const double* __restrict__
     const double* b_src = Bs[1];
     for (int64_t s = 0; s < slices; ++s) {
       const bool more = s + 1 < slices;
-      if (s + 2 < slices) load_slice((s + 2) * BK);
+      if (s + 2 < slices) load_slice((s + 2) * BK, int(s & 1));
 #pragma unroll
       for (int h = 0; h < 2; ++h) {
         const int a_read = h == 0 ? a_read0 : a_read1;
@@ -726,7 +787,7 @@ __global__ __launch_bounds__(kThreads, 1) void kernel(const double* __restrict__
       }
       a_src = (s & 1) ? As[1] : As[0];
       b_src = (s & 1) ? Bs[1] : Bs[0];
-      __syncthreads();
+      publish();
     }
 
     if (slot < 0) {
@@ -919,7 +980,12 @@ void run_f64(hp_ctx* ctx, const double* a, const double* b, double* c, int64_t m
   TileMap tm;
   prepare(m, n, batch, BM, BN, tm);
   auto fix = fixup_kernel<double, f64x4, Layout>;
-  switch (mode_of(m, n, k, BM, BN, BK)) {
+  int mode = mode_of(m, n, k, BM, BN, BK);
+  // Modes 0 and 1 load k-contiguous operands with LDS-DMA (16-byte aligned
+  // rows, as in run_f32); views at other element offsets use mode 2.
+  const bool aligned = (TA || reinterpret_cast<uintptr_t>(a) % 16 == 0) && (!TB || reinterpret_cast<uintptr_t>(b) % 16 == 0);
+  if (!aligned) mode = 2;
+  switch (mode) {
     case 0:
       launch_split<double, BM, BN>(ctx, kernel<0, false, TA, TB>, kernel<0, true, TA, TB>, fix, kThreads, a, b, c,
                                    m, n, k, bd, tm, BK, "gemm_f64", false);
