@@ -143,6 +143,25 @@ __device__ __forceinline__ double transform<double, kUniformScaled>(const Words&
   return value < first ? first : (value > upper ? upper : value);
 }
 
+// Pre-scaled uniform with first == 0 and a positive width w (the default
+// uniform()): the reference value clip(0 + w * u, 0, nextafter(w, 0)) is
+// k * scaled rounded once. The sum with 0 is exact, and the clip never
+// binds: k <= 2^b - 1 gives k * scaled = w (1 - 2^-b) at most, whose
+// distance below w is at least half an ulp of w, so it rounds to a float
+// below w (a power-of-two w leaves it exactly representable).
+constexpr int kUniformScaledZero = 5;
+
+template <>
+__device__ __forceinline__ float transform<float, kUniformScaledZero>(const Words& w, float, float scaled, float) {
+  return float(w.x0 >> 8) * scaled;
+}
+
+template <>
+__device__ __forceinline__ double transform<double, kUniformScaledZero>(const Words& w, double, double scaled,
+                                                                        double) {
+  return (double(w.x0 >> 5) * 67108864.0 + double(w.x1 >> 6)) * scaled;
+}
+
 template <typename T>
 __device__ __forceinline__ void store4(T* out, int64_t e0, int64_t count, const T (&v)[4]);
 
@@ -237,8 +256,13 @@ void launch(hp_ctx* ctx, int dist, T* out, int64_t count, uint32_t k0, uint32_t 
   hp::require(grid <= hp::kMaxGrid, "random output too large for one launch");
   T scaled;
   if (dist == HP_UNIFORM && uniform_scaled(first, second, upper, &scaled)) {
-    philox_kernel<T, kUniformScaled><<<grid, kBlock, 0, ctx->stream>>>(out, count, k0, k1, start, first, scaled,
-                                                                       upper);
+    if (first == 0 && scaled > 0) {
+      philox_kernel<T, kUniformScaledZero><<<grid, kBlock, 0, ctx->stream>>>(out, count, k0, k1, start, first,
+                                                                             scaled, upper);
+    } else {
+      philox_kernel<T, kUniformScaled><<<grid, kBlock, 0, ctx->stream>>>(out, count, k0, k1, start, first, scaled,
+                                                                         upper);
+    }
     hp::check_launch("philox");
     return;
   }

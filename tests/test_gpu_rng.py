@@ -99,6 +99,12 @@ UNIFORM_BOUNDS = [
     (-1.5e38, 1.5e38),
     (5e-324, 1e-322),
     (-2.0**-126, 2.0**-126),
+    # low == 0 with a positive width: the kernel without offset or clamp
+    (0.0, 3.7),
+    (0.0, 1e30),
+    (0.0, 3.4e38),
+    (0.0, 2.0**-100),
+    (-0.0, 5.5),
 ]
 
 
@@ -185,6 +191,17 @@ def test_config5_full_stream_2_28_random_is_bit_exact(hip):
     rng._counter = n
     tail = p.asnumpy(rng.uniform(size=4096, dtype="float32"))
     np.testing.assert_array_equal(tail, philox.c_uniform("float32", 4096, 42, n, "uniform", 0, 1))
+
+
+@pytest.mark.parametrize("high", [1.0, 3.7])
+def test_config5_full_size_uniform_from_zero_is_bit_exact(hip, high):
+    # 2^28 samples reach every 24-bit unit numerator, including the largest,
+    # so the unclamped uniform(0, w) kernel is checked where a clamp could bind.
+    n = 1 << 28
+    got = p.asnumpy(p.random.default_rng(42, backend=hip).uniform(0.0, high, n, dtype="float32"))
+    want = philox.c_uniform("float32", n, 42, 0, "uniform", 0.0, high)
+    assert np.array_equal(got.view(np.uint32), want.view(np.uint32))
+    assert got.max() < np.float32(high)
 
 
 def test_config5_full_size_normal_and_exponential_properties(hip):
