@@ -1,0 +1,53 @@
+"""bench.py's command-line contract on the CPU (no GPU is touched).
+
+One GPU only: ``--gpus`` above 1 exits with status 2 and a message before
+any backend is created. The roofline helper reports the fraction against
+MI355X's published peaks, and the PMC traffic and VALU tables it reads name
+kernels that exist in the built library.
+"""
+
+import json
+import subprocess
+import sys
+from pathlib import Path
+
+import pytest
+
+ROOT = Path(__file__).resolve().parents[1]
+sys.path.insert(0, str(ROOT))
+
+import bench  # noqa: E402
+
+
+@pytest.mark.parametrize("gpus", ["2", "8"])
+def test_more_than_one_gpu_exits_with_a_message(gpus):
+    done = subprocess.run(
+        [sys.executable, str(ROOT / "bench.py"), "--gpus", gpus], capture_output=True, text=True, timeout=120
+    )
+    assert done.returncode == 2
+    assert "one MI355X" in done.stderr and not done.stdout
+
+
+def test_roofline_fractions_use_published_peaks():
+    gemm = bench.roofline("mfma", 2 * 8192**3, 7.8)
+    assert gemm["peak"] == 157.3 and gemm["unit"] == "TFLOP/s"
+    assert gemm["frac"] == pytest.approx(2 * 8192**3 / 7.8e-3 / 1e12 / 157.3, rel=1e-3)
+    hbm = bench.roofline("hbm", 2**30, 0.157)
+    assert hbm["peak"] == 8000.0 and hbm["unit"] == "GB/s"
+    assert hbm["frac"] == pytest.approx(2**30 / 0.157e-3 / 1e9 / 8000.0, rel=1e-3)
+
+
+def test_profile_tables_name_built_kernels():
+    resources = ROOT / "open-pacho_amd" / "_build" / "resources.json"
+    if not resources.exists():
+        pytest.skip("library not built in this tree")
+    built = json.dumps(json.loads(resources.read_text()))
+    traffic = json.loads((ROOT / "profiles" / "traffic.json").read_text())
+    valu = json.loads((ROOT / "profiles" / "valu.json").read_text())
+    for table in (traffic, valu):
+        for name, entry in table.items():
+            if name.startswith("_"):
+                continue
+            kernel = entry["kernel"]  # e.g. "philox_kernel<float, 5>", "f32::kernel<0, false, false, false>"
+            base = kernel.split("<")[0].split("::")[-1]
+            assert base in built, (name, kernel)
