@@ -117,6 +117,8 @@ def test_batched_broadcast_products(hip, dtype, shapes):
         (31, 33, 4099),  # long K, partial tiles
         (640, 384, 48),  # M/N edges with K whole: edge tiles moved inside
         (777, 300, 64),  # moved edge tiles that own 9 rows / 44 columns
+        (257, 257, 32),  # moved edge tiles that own a single row / column
+        (513, 1023, 16),  # one K slice; edges of 1 row and 255 columns
     ],
 )
 def test_kernel_modes_against_float64(hip, dtype, m, n, k):
@@ -141,6 +143,7 @@ STREAM_K_CASES = [
     (np.float32, (), 777, 555, 1111),  # K odd
     (np.float32, (3,), 300, 200, 700),  # batched: 6 tiles
     (np.float32, (2,), 600, 300, 512),  # batched, moved edge tiles summed by the fixup
+    (np.float32, (), 257, 257, 4096),  # single-row/column moved tiles cut over many workers
     (np.float64, (), 1000, 1000, 2000),  # 32 tiles over 256 workers, extra > 0
     (np.float64, (2,), 256, 384, 1024),  # interior fp64, batched
     (np.float64, (), 129, 65, 3001),  # K odd, fp64
