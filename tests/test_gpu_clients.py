@@ -1,6 +1,6 @@
 """Application clients of the hot path on the hip backend.
 
-The reference ships two client families of this path (SURVEY next-step rows):
+The reference ships two client families of this path:
 a dense regression network trained by explicit SGD (reference
 examples/dense_network.py:50-77: tanh layer, transposed products for the
 gradients, row sums for bias gradients) and dense iterative solvers
