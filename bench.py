@@ -304,7 +304,10 @@ def bench_extras(p, hip, only, skip_cpu):
         n = 1 << 28
         for dist in ("uniform", "normal", "exponential"):
             rng = p.random.default_rng(42, backend=hip)
-            ms, wall = timer.run(lambda: getattr(rng, dist)(size=n, dtype="float32"), 10)
+            # Vector-ALU bound, so the rate follows the compute clock, which
+            # reaches its sustained value only after some tens of milliseconds
+            # of load: 200 untimed calls (~60 ms) first, then 100 timed.
+            ms, wall = timer.run(lambda: getattr(rng, dist)(size=n, dtype="float32"), 100, warmup=200)
             bytes_moved = n * 4
             extra[f"rng_{dist}_f32_2^28"] = {
                 "value": round(n / (ms * 1e-3) / 1e9, 2),
