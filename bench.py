@@ -30,10 +30,26 @@ METRIC = "fp32 GEMM GFLOP/s @8192³ + GEMV/norm HBM GB/s, % of MI355X roofline"
 PEAK_HBM_GBS = 8000.0
 PEAK_FP32_TFLOPS = 157.3
 PEAK_FP64_TFLOPS = 78.6
+# Untimed load before each extra workload. The MI355X raises its compute
+# clock only after some tens of milliseconds of sustained work: after an idle
+# second, 2 warm-up calls left fp64 4096^3 at 77-79% of peak against 85% once
+# warm, and the RNG at ~700 against ~900 Gsample/s.
+WARM_MS = 100.0
 
 
 def log(message):
     print(f"[bench] {message}", file=sys.stderr, flush=True)
+
+
+def warm(fn, synchronize, calls):
+    """Untimed calls: at least ``calls`` of them and at least WARM_MS of
+    device work, so that the timed region starts at the sustained clock."""
+    t0 = time.perf_counter()
+    done = 0
+    while done < calls or (time.perf_counter() - t0) * 1e3 < WARM_MS:
+        fn()
+        done += 1
+        synchronize()
 
 
 class Timer:
@@ -48,9 +64,7 @@ class Timer:
 
     def run(self, fn, reps, warmup=2):
         lib, ctx = self.backend._lib, self.backend._ctx
-        for _ in range(warmup):
-            fn()
-        self.backend.synchronize()
+        warm(fn, self.backend.synchronize, warmup)
         wall0 = time.perf_counter()
         lib.hp_event_record(ctx, self.start)
         for _ in range(reps):
@@ -206,9 +220,7 @@ def vendor_gemm_child():
         generator = torch.Generator(device="cuda").manual_seed(3)
         a = torch.rand((n, n), device="cuda", dtype=dtype, generator=generator) * 2 - 1
         b = torch.rand((n, n), device="cuda", dtype=dtype, generator=generator) * 2 - 1
-        for _ in range(3):
-            torch.matmul(a, b)
-        torch.cuda.synchronize()
+        warm(lambda: torch.matmul(a, b), torch.cuda.synchronize, 3)
         start, stop = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
         reps = 10
         start.record()
@@ -304,10 +316,7 @@ def bench_extras(p, hip, only, skip_cpu):
         n = 1 << 28
         for dist in ("uniform", "normal", "exponential"):
             rng = p.random.default_rng(42, backend=hip)
-            # Vector-ALU bound, so the rate follows the compute clock, which
-            # reaches its sustained value only after some tens of milliseconds
-            # of load: 200 untimed calls (~60 ms) first, then 100 timed.
-            ms, wall = timer.run(lambda: getattr(rng, dist)(size=n, dtype="float32"), 100, warmup=200)
+            ms, wall = timer.run(lambda: getattr(rng, dist)(size=n, dtype="float32"), 100)
             bytes_moved = n * 4
             extra[f"rng_{dist}_f32_2^28"] = {
                 "value": round(n / (ms * 1e-3) / 1e9, 2),
@@ -394,7 +403,7 @@ def main(argv=None):
     parser = argparse.ArgumentParser(description=__doc__.splitlines()[0])
     parser.add_argument("--gpus", type=int, default=1)
     parser.add_argument("--steps", type=int, default=10)
-    parser.add_argument("--warmup", type=int, default=3)
+    parser.add_argument("--warmup", type=int, default=15)
     parser.add_argument("--skip-cpu", action="store_true", help="omit the CPU baselines")
     parser.add_argument("--vendor-child", action="store_true", help=argparse.SUPPRESS)
     parser.add_argument("--only", default="", help="comma-separated extras to run (gemv,norm,rng,gemm_f64,gemm_padded,gemm_batched,mlp,vendor; copy = PMC calibration, only when named); 'none' for the headline only")
