@@ -3,7 +3,8 @@
 One GPU only: ``--gpus`` above 1 exits with status 2 and a message before
 any backend is created. The roofline helper reports the fraction against
 MI355X's published peaks, and the PMC traffic and VALU tables it reads name
-kernels that exist in the built library.
+kernels that exist in the built library. Every timed workload is preceded by
+at least a minimum number of untimed calls and a minimum span of untimed work.
 """
 
 import json
@@ -51,3 +52,17 @@ def test_profile_tables_name_built_kernels():
             kernel = entry["kernel"]  # e.g. "philox_kernel<float, 5>", "f32::kernel<0, false, false, false>"
             base = kernel.split("<")[0].split("::")[-1]
             assert base in built, (name, kernel)
+
+
+def test_warm_up_runs_the_minimum_calls_and_the_minimum_time(monkeypatch):
+    monkeypatch.setattr(bench, "WARM_MS", 30.0)
+    calls, syncs = [], []
+    start = bench.time.perf_counter()
+    bench.warm(lambda: calls.append(1), lambda: syncs.append(1), 3)
+    elapsed_ms = (bench.time.perf_counter() - start) * 1e3
+    assert len(calls) >= 3 and len(syncs) == len(calls)
+    assert elapsed_ms >= 30.0
+    monkeypatch.setattr(bench, "WARM_MS", 0.0)
+    calls.clear()
+    bench.warm(lambda: calls.append(1), lambda: None, 5)
+    assert len(calls) == 5
