@@ -12,7 +12,7 @@ needs only ``ndarray`` from the array facade.
 On this backend padding turns an unaligned problem (e.g. odd K, which forces
 scalar guarded loads) into the 16-byte vector-load path of the MFMA kernel.
 ``bounds_checks_removed`` is True only when the padded problem is a whole
-number of the kernel's workgroup tiles (256 x 16 x 128), because only then
+number of the kernel's workgroup tiles (256 x 16 x 256), because only then
 does the GEMM run without element guards.
 """
 
