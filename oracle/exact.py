@@ -10,7 +10,7 @@
   power-of-two scaling (64-bit significand, exponent range covers squares of
   1e+-300), used for full-size fp64 norms.
 - norm_exact: exact sum of squares with integers, square root rounded once.
-Pinned by tests/test_oracle_exact.py (closed forms, Pythagorean triples,
+Pinned by tests/test_oracle_kernels.py (closed forms, Pythagorean triples,
 cancellation cases whose exact value is known, agreement with math.fsum).
 """
 

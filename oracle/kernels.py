@@ -8,6 +8,7 @@ north-star bar scales (hip error <= 2x this).
 
 - gemm_sequential: _gemm.py:67-77 (fp32 register tile: K ascending, c += a*b)
   and _cuda.py:619-636 (direct fp64 kernel: same order in binary64).
+  gemm_sequential_rows is the same order for whole rows of the product.
 - gemv_lanes:      _cuda_gemv.py:35-43 (lane l sums j = l (mod 128) in order,
   then shared tree 64 -> 1), with DOT chunks of 1024 for 1-D K > 4096
   (:67-84) reduced by reduce_lanes.
@@ -36,6 +37,22 @@ def gemm_sequential(a, b, rows, cols):
         for k in range(a.shape[1]):
             product = np.multiply(a[rows, k], b[k, cols], dtype=dt)
             acc = np.add(acc, product, dtype=dt)
+    return acc
+
+
+def gemm_sequential_rows(a_rows, b):
+    """a_rows @ b (2-D) in the sequential-K order, every row of the block.
+
+    The same rounding sequence as gemm_sequential (c += a[:, k] * b[k, :],
+    k ascending, product and sum rounded separately), vectorised over a row
+    block instead of over sampled coordinates.
+    """
+    a_rows, b = np.asarray(a_rows), np.asarray(b)
+    dt = np.result_type(a_rows.dtype, b.dtype)
+    acc = np.zeros((a_rows.shape[0], b.shape[1]), dtype=dt)
+    with np.errstate(all="ignore"):
+        for k in range(a_rows.shape[1]):
+            acc += np.multiply(a_rows[:, k, None], b[k, None, :], dtype=dt)
     return acc
 
 

@@ -7,7 +7,7 @@ reference of the reference's own conformance tests:
             output dtype, 0 where scale == 0; scale*sqrt(total); inf scale
             gives inf).
 - random:   reference _random.py:34-58 (_numpy_data), via oracle.philox.
-Pinned by tests/test_oracle_numpy_backend.py: golden samples and norms written
+Pinned by tests/test_oracle_kernels.py and tests/test_oracle_philox.py: golden samples and norms written
 from the reference NumPy backend (tests/golden/), closed forms (Pythagorean
 triples, constant vectors), and the special-value table of reference
 tests/test_stable_norm.py:60-66.

@@ -278,6 +278,8 @@ def test_config4_batched_broadcast(hip):
     for batch in (0, 31, 63):
         want = a[batch].astype(np.float64) @ b.astype(np.float64)
         np.testing.assert_allclose(got[batch], want, rtol=0, atol=2e-4)
+        hip_err, ref_err = _sampled_error_ratio(a[batch], b, got[batch], 32, 9 + batch)
+        assert hip_err <= 2 * ref_err, f"batch {batch}: {hip_err} > 2 x {ref_err}"
 
 
 @pytest.mark.parametrize("shapes", [((33, 17), (17, 65)), ((65, 47), (47, 67)), ((64, 32), (32, 96)), ((2, 1, 33, 17), (1, 3, 17, 65))])

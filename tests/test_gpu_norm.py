@@ -131,9 +131,10 @@ def test_config3_row_norms_full_size(hip):
 
 @pytest.mark.parametrize("dtype", [np.float32, np.float64])
 def test_flat_norm_single_pass_repeats_across_grid_sizes(hip, dtype):
-    # The single-row kernel's last workgroup merges every workgroup's pair
-    # and resets the completion counter: calls of different grid sizes in a
-    # row must each see a fresh count, and repeats are bitwise identical.
+    # A flat norm is a row pass that writes one (exponent, sum) pair per
+    # wave plus a merge launch over those pairs: calls of different grid
+    # sizes in a row reuse the partial buffer and repeats are bitwise
+    # identical.
     rng = np.random.default_rng(17)
     sizes = [1 << 22, 5000, 3 * 4096 + 1, 1 << 20, 2, (1 << 24) + 7]
     hosts = [rng.uniform(-1, 1, n).astype(dtype) for n in sizes]

@@ -71,6 +71,23 @@ def test_gemm_sequential_is_the_sequential_float32_loop():
     assert kernels.gemm_sequential(ints, ints.T.copy(), [2], [1])[0] == float(ints[2] @ ints[1])
 
 
+def test_gemm_sequential_rows_is_the_sampled_order_on_every_coordinate():
+    rng = np.random.default_rng(2)
+    for dtype in (np.float32, np.float64):
+        a = rng.uniform(-1, 1, (7, 129)).astype(dtype)
+        b = rng.uniform(-1, 1, (129, 11)).astype(dtype)
+        rows, cols = np.meshgrid(range(7), range(11), indexing="ij")
+        sampled = kernels.gemm_sequential(a, b, rows.ravel(), cols.ravel()).reshape(7, 11)
+        block = kernels.gemm_sequential_rows(a, b)
+        assert block.dtype == dtype
+        np.testing.assert_array_equal(block.view(np.uint8), sampled.view(np.uint8))
+    # A transposed operand or a dropped product would change the exact
+    # integer result of a non-symmetric case.
+    left = np.arange(6, dtype=np.float32).reshape(2, 3)
+    right = np.arange(12, dtype=np.float32).reshape(3, 4) - 5
+    np.testing.assert_array_equal(kernels.gemm_sequential_rows(left, right), left.astype(np.float64) @ right)
+
+
 def test_gemv_lanes_order_and_exact_cases():
     x = np.arange(1, 301, dtype=np.float64)
     assert kernels.gemv_lanes(x, np.ones(300)) == 300 * 301 / 2
