@@ -194,6 +194,24 @@ int hp_dot(hp_ctx* ctx, int dtype, const void* x, const void* y, void* out, int6
 int hp_norm(hp_ctx* ctx, int dtype, const void* x, void* out, int64_t outer, int64_t reduced,
             int64_t inner);
 
+/* Size of the static device workspace of hp_norm_noalloc, per GPU. */
+#define HP_NORM_NOALLOC_SCRATCH_BYTES (4 << 20)
+
+/* hp_norm with the same kernels and results (bit for bit), but it allocates
+ * nothing: no hipMalloc/hipFree, no pool block, no memset node. Its
+ * temporaries (the per-chunk pairs and merge partials) live in a static
+ * device array of HP_NORM_NOALLOC_SCRATCH_BYTES per GPU, held until the
+ * process ends. A shape whose temporaries exceed it fails with HP_E_INVALID
+ * before any launch (contiguous f32 rows up to ~2^31 elements fit).
+ * Every call on one GPU shares that GPU's array, so calls whose work overlaps
+ * on one GPU (two contexts' streams, or threads without ordering) race; calls
+ * on one context are ordered by its stream and do not.
+ * No counterpart in the reference: it is for callers that cannot allocate
+ * (code under HIP graph capture, tight serving loops, harnesses that forbid
+ * hipMalloc). */
+int hp_norm_noalloc(hp_ctx* ctx, int dtype, const void* x, void* out, int64_t outer, int64_t reduced,
+                    int64_t inner);
+
 /* out[o*inner + i] = op_r x[(o*reduced + r)*inner + i] for op in
  * {HP_SUM, HP_MIN, HP_MAX}. Sum: any numeric dtype except bool. Min/max:
  * NaN propagates, min prefers -0 and max prefers +0 on zero ties.

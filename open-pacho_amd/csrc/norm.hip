@@ -280,57 +280,161 @@ __global__ __launch_bounds__(kBlock) void norm_cols_kernel(const T* __restrict__
   }
 }
 
+// Temporary device memory of one norm call: the pair buffer the row pass
+// writes (`first` bytes) and the output of the first of two or more merge
+// passes (`second` bytes). Later merge passes alternate between the two: a
+// pass only reads the buffer the previous pass wrote.
+struct Workspace {
+  void* first = nullptr;
+  void* second = nullptr;
+};
+
+struct RowPlan {
+  int mode = kFinal;
+  bool vector = false;
+  int64_t chunks = 0, grid = 0;
+  int64_t pairs = 0;   // pairs the row pass writes (0 in kFinal mode)
+  int64_t second = 0;  // pairs the first merge pass writes when it is not the last
+};
+
 template <typename T>
-void run_norm(hp_ctx* ctx, const T* x, T* out, int64_t outer, int64_t reduced, int64_t inner) {
-  if (inner > 1) {
-    const int64_t work = outer * inner;
-    int64_t grid = hp::ceil_div(work, kBlock);
-    if (grid > 65536 * 4) grid = 65536 * 4;
-    norm_cols_kernel<T><<<grid, kBlock, 0, ctx->stream>>>(x, out, outer, reduced, inner);
-    hp::check_launch("norm_cols");
-    return;
-  }
-  const int64_t chunks = hp::ceil_div(reduced, chunk_len<T>());
-  const int64_t units = outer * chunks;
-  const bool vector = reinterpret_cast<uintptr_t>(x) % 16 == 0 && (reduced * int64_t(sizeof(T))) % 16 == 0;
-  const int mode = chunks == 1 ? kFinal : (outer == 1 ? kRunning : kPairs);
+RowPlan plan_rows(hp_ctx* ctx, const T* x, int64_t outer, int64_t reduced) {
+  RowPlan plan;
+  plan.chunks = hp::ceil_div(reduced, chunk_len<T>());
+  const int64_t units = outer * plan.chunks;
+  plan.vector = reinterpret_cast<uintptr_t>(x) % 16 == 0 && (reduced * int64_t(sizeof(T))) % 16 == 0;
+  plan.mode = plan.chunks == 1 ? kFinal : (outer == 1 ? kRunning : kPairs);
   // Enough resident waves to keep HBM busy; the grid loops over the rest.
   const int64_t resident = int64_t(ctx->compute_units) * kResidentGroupsPerCU;
-  int64_t grid = hp::ceil_div(units, kBlock / 64);
-  if (grid > resident) grid = resident;
-  T* pairs = nullptr;
-  T* target = out;
-  int64_t remaining = 1;
-  if (mode != kFinal) {
-    remaining = mode == kRunning ? grid : chunks;
-    pairs = static_cast<T*>(hp::scratch_alloc(ctx, size_t(mode == kRunning ? grid : units) * 2 * sizeof(T)));
-    target = pairs;
+  plan.grid = hp::ceil_div(units, kBlock / 64);
+  if (plan.grid > resident) plan.grid = resident;
+  if (plan.mode != kFinal) {
+    const int64_t per_row = plan.mode == kRunning ? plan.grid : plan.chunks;
+    plan.pairs = plan.mode == kRunning ? plan.grid : units;
+    const int64_t groups = hp::ceil_div(per_row, kMerge);
+    plan.second = groups > 1 ? outer * groups : 0;
   }
+  return plan;
+}
+
+template <typename T>
+void run_rows(hp_ctx* ctx, const RowPlan& plan, const T* x, T* out, int64_t outer, int64_t reduced,
+              Workspace ws) {
+  const int64_t grid = plan.grid, chunks = plan.chunks;
+  T* target = plan.mode == kFinal ? out : static_cast<T*>(ws.first);
 #define PACHO_NORM_LAUNCH(VEC, MODE_)                                                                           \
   norm_rows_kernel<T, VEC, MODE_><<<grid, kBlock, 0, ctx->stream>>>(x, target, outer, reduced, chunks)
-  if (vector) {
-    if (mode == kFinal) PACHO_NORM_LAUNCH(true, kFinal);
-    else if (mode == kRunning) PACHO_NORM_LAUNCH(true, kRunning);
+  if (plan.vector) {
+    if (plan.mode == kFinal) PACHO_NORM_LAUNCH(true, kFinal);
+    else if (plan.mode == kRunning) PACHO_NORM_LAUNCH(true, kRunning);
     else PACHO_NORM_LAUNCH(true, kPairs);
   } else {
-    if (mode == kFinal) PACHO_NORM_LAUNCH(false, kFinal);
-    else if (mode == kRunning) PACHO_NORM_LAUNCH(false, kRunning);
+    if (plan.mode == kFinal) PACHO_NORM_LAUNCH(false, kFinal);
+    else if (plan.mode == kRunning) PACHO_NORM_LAUNCH(false, kRunning);
     else PACHO_NORM_LAUNCH(false, kPairs);
   }
 #undef PACHO_NORM_LAUNCH
   hp::check_launch("norm_rows");
+  if (plan.mode == kFinal) return;
   // Pair modes always finish with at least one merge pass (it writes `out`).
-  while (mode != kFinal && (pairs != out)) {
+  T* source = static_cast<T*>(ws.first);
+  T* spare = static_cast<T*>(ws.second);
+  int64_t remaining = plan.mode == kRunning ? grid : chunks;
+  for (;;) {
     const int64_t groups = hp::ceil_div(remaining, kMerge);
     const bool last = groups == 1;
-    T* next = last ? out : static_cast<T*>(hp::scratch_alloc(ctx, size_t(outer * groups) * 2 * sizeof(T)));
+    T* next = last ? out : spare;
     hp::require(outer * groups <= hp::kMaxGrid, "too many rows for one launch");
-    norm_merge_kernel<T><<<outer * groups, kBlock, 0, ctx->stream>>>(pairs, next, remaining, groups, last);
+    norm_merge_kernel<T><<<outer * groups, kBlock, 0, ctx->stream>>>(source, next, remaining, groups, last);
     hp::check_launch("norm_merge");
-    hp::scratch_free(ctx, pairs);
-    pairs = next;
+    if (last) return;
+    spare = source;
+    source = next;
     remaining = groups;
   }
+}
+
+template <typename T>
+void run_cols(hp_ctx* ctx, const T* x, T* out, int64_t outer, int64_t reduced, int64_t inner) {
+  const int64_t work = outer * inner;
+  int64_t grid = hp::ceil_div(work, kBlock);
+  if (grid > 65536 * 4) grid = 65536 * 4;
+  norm_cols_kernel<T><<<grid, kBlock, 0, ctx->stream>>>(x, out, outer, reduced, inner);
+  hp::check_launch("norm_cols");
+}
+
+// hp_norm: the workspace comes from the context's stream-ordered pool and goes
+// back to it as soon as the launches that use it are queued.
+template <typename T>
+void run_norm(hp_ctx* ctx, const T* x, T* out, int64_t outer, int64_t reduced, int64_t inner) {
+  if (inner > 1) return run_cols<T>(ctx, x, out, outer, reduced, inner);
+  const RowPlan plan = plan_rows<T>(ctx, x, outer, reduced);
+  Workspace ws;
+  if (plan.pairs > 0) ws.first = hp::scratch_alloc(ctx, size_t(plan.pairs) * 2 * sizeof(T));
+  if (plan.second > 0) ws.second = hp::scratch_alloc(ctx, size_t(plan.second) * 2 * sizeof(T));
+  run_rows<T>(ctx, plan, x, out, outer, reduced, ws);
+  if (ws.second) hp::scratch_free(ctx, ws.second);
+  if (ws.first) hp::scratch_free(ctx, ws.first);
+}
+
+// ---- allocation-free variant ---------------------------------------------
+//
+// hp_norm_noalloc keeps its workspace in `scratch`, a fixed device array that
+// every GPU the library runs on holds until the process ends. Host code never
+// passes the array's name to a kernel (on the host it is only a stand-in for
+// the symbol): the device address comes from hipGetSymbolAddress, looked up
+// once per device with that device current, and only that address is used.
+
+constexpr size_t kAlign = 256;
+inline size_t align_up(size_t bytes) { return (bytes + kAlign - 1) / kAlign * kAlign; }
+
+template <typename T>
+__global__ __launch_bounds__(kBlock) void zero_kernel(T* __restrict__ out, int64_t count) {
+  const int64_t stride = int64_t(gridDim.x) * kBlock;
+  for (int64_t i = int64_t(blockIdx.x) * kBlock + threadIdx.x; i < count; i += stride) out[i] = T(0);
+}
+
+}  // namespace
+
+static __device__ __align__(256) unsigned char scratch[HP_NORM_NOALLOC_SCRATCH_BYTES];
+
+namespace {
+
+std::mutex g_scratch_mutex;
+std::unordered_map<int, void*> g_scratch_address;  // device -> address of `scratch`
+
+// Device address of `scratch` on ctx->device (current after hp::enter).
+void* scratch_address(hp_ctx* ctx) {
+  std::lock_guard<std::mutex> lock(g_scratch_mutex);
+  auto found = g_scratch_address.find(ctx->device);
+  if (found != g_scratch_address.end()) return found->second;
+  void* address = nullptr;
+  HP_CHECK(hipGetSymbolAddress(&address, HIP_SYMBOL(scratch)));
+  hp::require(address != nullptr && reinterpret_cast<uintptr_t>(address) % kAlign == 0,
+              "scratch symbol has no aligned device address");
+  g_scratch_address.emplace(ctx->device, address);
+  return address;
+}
+
+template <typename T>
+void run_norm_noalloc(hp_ctx* ctx, const T* x, T* out, int64_t outer, int64_t reduced, int64_t inner) {
+  if (inner > 1) return run_cols<T>(ctx, x, out, outer, reduced, inner);
+  const RowPlan plan = plan_rows<T>(ctx, x, outer, reduced);
+  const size_t first = align_up(size_t(plan.pairs) * 2 * sizeof(T));
+  const size_t second = size_t(plan.second) * 2 * sizeof(T);
+  if (first + second > HP_NORM_NOALLOC_SCRATCH_BYTES) {
+    hp::fail(HP_E_INVALID, "hp_norm_noalloc: this shape needs " + std::to_string(first + second) +
+                               " bytes of workspace, more than the " +
+                               std::to_string(HP_NORM_NOALLOC_SCRATCH_BYTES) +
+                               "-byte static scratch; call hp_norm");
+  }
+  Workspace ws;
+  if (first + second > 0) {
+    char* base = static_cast<char*>(scratch_address(ctx));
+    ws.first = base;
+    ws.second = base + first;
+  }
+  run_rows<T>(ctx, plan, x, out, outer, reduced, ws);
 }
 
 }  // namespace
@@ -357,6 +461,33 @@ int hp_norm(hp_ctx* ctx, int dtype, const void* x, void* out, int64_t outer, int
       run_norm<float>(ctx, (const float*)x, (float*)out, outer, reduced, inner);
     } else {
       run_norm<double>(ctx, (const double*)x, (double*)out, outer, reduced, inner);
+    }
+  });
+}
+
+int hp_norm_noalloc(hp_ctx* ctx, int dtype, const void* x, void* out, int64_t outer, int64_t reduced,
+                    int64_t inner) {
+  return guarded([&] {
+    hp::enter(ctx);
+    require(dtype == HP_F32 || dtype == HP_F64, "norm supports float32 and float64");
+    require(outer >= 0 && reduced >= 0 && inner >= 0, "negative extent");
+    const int64_t count = outer * inner;
+    if (count == 0) return;
+    require(out != nullptr, "null output");
+    if (reduced == 0) {
+      // A fill kernel rather than hipMemsetAsync, so the call can be captured.
+      int64_t grid = hp::ceil_div(count, kBlock);
+      if (grid > 65536) grid = 65536;
+      if (dtype == HP_F32) zero_kernel<float><<<grid, kBlock, 0, ctx->stream>>>((float*)out, count);
+      else zero_kernel<double><<<grid, kBlock, 0, ctx->stream>>>((double*)out, count);
+      hp::check_launch("norm_zero");
+      return;
+    }
+    require(x != nullptr, "null input");
+    if (dtype == HP_F32) {
+      run_norm_noalloc<float>(ctx, (const float*)x, (float*)out, outer, reduced, inner);
+    } else {
+      run_norm_noalloc<double>(ctx, (const double*)x, (double*)out, outer, reduced, inner);
     }
   });
 }

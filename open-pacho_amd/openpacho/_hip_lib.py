@@ -59,6 +59,7 @@ PROTOTYPES = {
     "hp_gemv_residual": [_ptr, _i32, _ptr, _ptr, _ptr, _ptr, _i64, _i64],
     "hp_dot": [_ptr, _i32, _ptr, _ptr, _ptr, _i64],
     "hp_norm": [_ptr, _i32, _ptr, _ptr, _i64, _i64, _i64],
+    "hp_norm_noalloc": [_ptr, _i32, _ptr, _ptr, _i64, _i64, _i64],
     "hp_reduce": [_ptr, _i32, _i32, _ptr, _ptr, _i64, _i64, _i64],
     "hp_philox": [_ptr, _i32, _i32, _ptr, _i64, _u64, _u64, ctypes.c_double, ctypes.c_double, ctypes.c_double],
     "hp_philox_words": [_ptr, _ptr, _i64, _u64, _u64],
