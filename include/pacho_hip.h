@@ -195,14 +195,16 @@ int hp_norm(hp_ctx* ctx, int dtype, const void* x, void* out, int64_t outer, int
             int64_t inner);
 
 /* Size of the static device workspace of hp_norm_noalloc, per GPU. */
-#define HP_NORM_NOALLOC_SCRATCH_BYTES (4 << 20)
+#define HP_NORM_NOALLOC_SCRATCH_BYTES (16 << 20)
 
 /* hp_norm with the same kernels and results (bit for bit), but it allocates
  * nothing: no hipMalloc/hipFree, no pool block, no memset node. Its
  * temporaries (the per-chunk pairs and merge partials) live in a static
  * device array of HP_NORM_NOALLOC_SCRATCH_BYTES per GPU, held until the
  * process ends. A shape whose temporaries exceed it fails with HP_E_INVALID
- * before any launch (contiguous f32 rows up to ~2^31 elements fit).
+ * before any launch (every contiguous f32 shape within the 2^31-element
+ * array cap fits, and every strided shape: their first partial array is
+ * planned below 8 MiB).
  * Every call on one GPU shares that GPU's array, so calls whose work overlaps
  * on one GPU (two contexts' streams, or threads without ordering) race; calls
  * on one context are ordered by its stream and do not.

@@ -13,6 +13,7 @@
 // Reference semantics: _norm.py:28-36 (NaN beats Inf, Inf -> Inf, zeros -> +0),
 // _norm.py:44-52 (two-pass max-scale closed form), linalg.py:8-35.
 #include "common.h"
+#include "strided.h"
 
 namespace {
 
@@ -248,36 +249,77 @@ __global__ __launch_bounds__(kBlock) void norm_merge_kernel(const T* __restrict_
   }
 }
 
-// Strided reduction axis (inner > 1): one thread per output, two passes over
-// the column (max, then compensated scaled sum of squares); lanes read
-// adjacent columns, so every load instruction is coalesced.
+// Strided reduction axis (inner > 1): the column engine of strided.h with
+// per-column pairs. A thread loads kBatch rows of its column into registers
+// and forms their pair exactly as a wave does for a contiguous chunk (max,
+// exponent, scaled sum of squares), so every element is read from HBM once;
+// pairs then merge across batches, rows of a step, chunks and passes.
 template <typename T>
-__global__ __launch_bounds__(kBlock) void norm_cols_kernel(const T* __restrict__ x, T* __restrict__ out,
-                                                           int64_t outer, int64_t reduced, int64_t inner) {
-  const int64_t stride = int64_t(gridDim.x) * blockDim.x;
-  for (int64_t g = int64_t(blockIdx.x) * blockDim.x + threadIdx.x; g < outer * inner; g += stride) {
-    const int64_t o = g / inner, i = g - o * inner;
-    const T* base = x + o * reduced * inner + i;
-    T m = T(0);
-    for (int64_t r = 0; r < reduced; ++r) m = nan_max(dabs(base[r * inner]), m);
-    T result;
-    if (isnan(m) || isinf(m) || m == T(0)) {
-      result = m;
-    } else {
-      // Neumaier-compensated sum: one thread walks the whole strided column.
-      const int e = dexponent(m);
-      T t = T(0), carry = T(0);
-      for (int64_t r = 0; r < reduced; ++r) {
-        const T s = dldexp(base[r * inner], -e);
-        const T term = s * s;
-        const T next = t + term;
-        carry += (t >= term) ? (t - next) + term : (term - next) + t;
-        t = next;
-      }
-      result = dldexp(dsqrt(t + carry), e);
-    }
-    out[g] = result;
+__device__ __forceinline__ Pair<T> lane_pair(const T* v, int n) {
+  T m = T(0);
+  for (int i = 0; i < n; ++i) m = dmax(m, dabs(v[i]));
+  if (isinf(m) || m == T(0)) {
+    bool nan = false;
+    for (int i = 0; i < n; ++i) nan = nan || isnan(v[i]);
+    if (nan) return {T(NAN), T(0)};
+    return isinf(m) ? Pair<T>{T(INFINITY), T(0)} : Pair<T>{T(-INFINITY), T(0)};
   }
+  const int e = dexponent(m);
+  T t = T(0);
+  for (int i = 0; i < n; ++i) {
+    const T s = dldexp(v[i], -e);
+    t = dfma(s, s, t);
+  }
+  if (isnan(t)) return {T(NAN), T(0)};
+  return {T(e), t};
+}
+
+template <typename T>
+struct NormColumns {
+  using In = T;
+  using Acc = Pair<T>;
+  using Out = T;
+  static constexpr int kBatch = 16;
+  __device__ static T identity_in() { return T(0); }  // a zero adds nothing to a pair
+  __device__ static Pair<T> identity() { return {T(-INFINITY), T(0)}; }
+  __device__ static Pair<T> fold(Pair<T> acc, const T (&v)[kBatch]) {
+    return merge(acc, lane_pair<T>(v, kBatch));
+  }
+  __device__ static Pair<T> combine(Pair<T> a, Pair<T> b) { return merge(a, b); }
+  __device__ static T finish(Pair<T> p) { return ::finish(p); }
+};
+
+template <typename T>
+struct NormPairColumns {
+  using In = Pair<T>;
+  using Acc = Pair<T>;
+  using Out = T;
+  static constexpr int kBatch = 8;
+  __device__ static Pair<T> identity_in() { return {T(-INFINITY), T(0)}; }
+  __device__ static Pair<T> identity() { return {T(-INFINITY), T(0)}; }
+  __device__ static Pair<T> fold(Pair<T> acc, const Pair<T> (&v)[kBatch]) {
+#pragma unroll
+    for (int j = 0; j < kBatch; ++j) acc = merge(acc, v[j]);
+    return acc;
+  }
+  __device__ static Pair<T> combine(Pair<T> a, Pair<T> b) { return merge(a, b); }
+  __device__ static T finish(Pair<T> p) { return ::finish(p); }
+};
+
+template <typename T>
+hps::Plan plan_cols(hp_ctx* ctx, const T* x, int64_t outer, int64_t reduced, int64_t inner) {
+  const int v_in = hps::vector_width(x, inner, sizeof(T));
+  const int v_acc = hps::vector_width(reinterpret_cast<const void*>(256), inner, sizeof(Pair<T>));
+  return hps::plan(outer, reduced, inner, v_in, v_acc, sizeof(Pair<T>), ctx->compute_units);
+}
+
+template <typename T>
+void run_cols(hp_ctx* ctx, const hps::Plan& plan, const T* x, T* out, int64_t outer, int64_t reduced,
+              int64_t inner, void* const buffers[2]) {
+  constexpr int v_in = sizeof(T) == 4 ? 4 : 2;
+  constexpr int v_acc = sizeof(Pair<T>) == 8 ? 2 : 1;
+  hps::execute<NormColumns<T>, NormPairColumns<T>, v_in, v_acc>(ctx->stream, plan, x, out, outer, reduced, inner,
+                                                                 buffers);
 }
 
 // Temporary device memory of one norm call: the pair buffer the row pass
@@ -354,20 +396,20 @@ void run_rows(hp_ctx* ctx, const RowPlan& plan, const T* x, T* out, int64_t oute
   }
 }
 
-template <typename T>
-void run_cols(hp_ctx* ctx, const T* x, T* out, int64_t outer, int64_t reduced, int64_t inner) {
-  const int64_t work = outer * inner;
-  int64_t grid = hp::ceil_div(work, kBlock);
-  if (grid > 65536 * 4) grid = 65536 * 4;
-  norm_cols_kernel<T><<<grid, kBlock, 0, ctx->stream>>>(x, out, outer, reduced, inner);
-  hp::check_launch("norm_cols");
-}
-
 // hp_norm: the workspace comes from the context's stream-ordered pool and goes
 // back to it as soon as the launches that use it are queued.
 template <typename T>
 void run_norm(hp_ctx* ctx, const T* x, T* out, int64_t outer, int64_t reduced, int64_t inner) {
-  if (inner > 1) return run_cols<T>(ctx, x, out, outer, reduced, inner);
+  if (inner > 1) {
+    const hps::Plan plan = plan_cols<T>(ctx, x, outer, reduced, inner);
+    void* buffers[2] = {nullptr, nullptr};
+    for (int i = 0; i < 2; ++i)
+      if (plan.bytes[i] > 0) buffers[i] = hp::scratch_alloc(ctx, plan.bytes[i]);
+    run_cols<T>(ctx, plan, x, out, outer, reduced, inner, buffers);
+    for (int i = 0; i < 2; ++i)
+      if (buffers[i]) hp::scratch_free(ctx, buffers[i]);
+    return;
+  }
   const RowPlan plan = plan_rows<T>(ctx, x, outer, reduced);
   Workspace ws;
   if (plan.pairs > 0) ws.first = hp::scratch_alloc(ctx, size_t(plan.pairs) * 2 * sizeof(T));
@@ -416,18 +458,34 @@ void* scratch_address(hp_ctx* ctx) {
   return address;
 }
 
-template <typename T>
-void run_norm_noalloc(hp_ctx* ctx, const T* x, T* out, int64_t outer, int64_t reduced, int64_t inner) {
-  if (inner > 1) return run_cols<T>(ctx, x, out, outer, reduced, inner);
-  const RowPlan plan = plan_rows<T>(ctx, x, outer, reduced);
-  const size_t first = align_up(size_t(plan.pairs) * 2 * sizeof(T));
-  const size_t second = size_t(plan.second) * 2 * sizeof(T);
+// Both workspace halves inside the static array, or a clear error.
+void check_scratch(size_t first, size_t second) {
   if (first + second > HP_NORM_NOALLOC_SCRATCH_BYTES) {
     hp::fail(HP_E_INVALID, "hp_norm_noalloc: this shape needs " + std::to_string(first + second) +
                                " bytes of workspace, more than the " +
                                std::to_string(HP_NORM_NOALLOC_SCRATCH_BYTES) +
                                "-byte static scratch; call hp_norm");
   }
+}
+
+template <typename T>
+void run_norm_noalloc(hp_ctx* ctx, const T* x, T* out, int64_t outer, int64_t reduced, int64_t inner) {
+  if (inner > 1) {
+    const hps::Plan plan = plan_cols<T>(ctx, x, outer, reduced, inner);
+    const size_t first = align_up(plan.bytes[0]);
+    check_scratch(first, plan.bytes[1]);
+    void* buffers[2] = {nullptr, nullptr};
+    if (first + plan.bytes[1] > 0) {
+      char* base = static_cast<char*>(scratch_address(ctx));
+      buffers[0] = base;
+      buffers[1] = base + first;
+    }
+    return run_cols<T>(ctx, plan, x, out, outer, reduced, inner, buffers);
+  }
+  const RowPlan plan = plan_rows<T>(ctx, x, outer, reduced);
+  const size_t first = align_up(size_t(plan.pairs) * 2 * sizeof(T));
+  const size_t second = size_t(plan.second) * 2 * sizeof(T);
+  check_scratch(first, second);
   Workspace ws;
   if (first + second > 0) {
     char* base = static_cast<char*>(scratch_address(ctx));

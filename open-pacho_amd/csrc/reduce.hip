@@ -8,12 +8,16 @@
 // Contiguous rows are reduced by one 256-thread workgroup per (row, chunk of
 // kChunk elements): lane-strided accumulation, a 64-lane butterfly and a
 // fixed-order merge of the four wave results. Rows longer than kChunk leave
-// one partial per chunk and are reduced again. Strided axes use one thread
-// per output element.
+// one partial per chunk and are reduced again. Strided axes (inner > 1) go
+// through the chunked column engine of strided.h.
+//
+// Signed integer sums add as the matching unsigned type (wrapping modulo
+// 2^bits, as NumPy does) so that overflow is never undefined behaviour.
 #include <limits>
 #include <type_traits>
 
 #include "common.h"
+#include "strided.h"
 
 namespace {
 
@@ -26,7 +30,14 @@ struct Combine;
 template <typename T>
 struct Combine<T, HP_SUM> {
   __device__ static T identity() { return T(0); }
-  __device__ static T apply(T a, T b) { return a + b; }
+  __device__ static T apply(T a, T b) {
+    if constexpr (std::is_integral<T>::value && std::is_signed<T>::value) {
+      using U = typename std::make_unsigned<T>::type;
+      return T(U(a) + U(b));
+    } else {
+      return a + b;
+    }
+  }
 };
 
 template <typename T>
@@ -131,41 +142,47 @@ __global__ __launch_bounds__(kBlock) void reduce_rows_kernel(const T* __restrict
   }
 }
 
+// Strided-axis op for the column engine: rows fold in ascending order.
 template <typename T, int OP>
-__global__ __launch_bounds__(kBlock) void reduce_cols_kernel(const T* __restrict__ x, T* __restrict__ out,
-                                                             int64_t outer, int64_t reduced, int64_t inner) {
+struct ColumnOp {
+  using In = T;
+  using Acc = T;
+  using Out = T;
   using C = Combine<T, OP>;
-  const int64_t stride = int64_t(gridDim.x) * blockDim.x;
-  for (int64_t g = int64_t(blockIdx.x) * blockDim.x + threadIdx.x; g < outer * inner; g += stride) {
-    const int64_t o = g / inner, i = g - o * inner;
-    const T* base = x + o * reduced * inner + i;
-    if constexpr (OP == HP_SUM && std::is_floating_point<T>::value) {
-      // Neumaier-compensated sum: one thread walks the whole strided column.
-      T acc = T(0), carry = T(0);
-      for (int64_t r = 0; r < reduced; ++r) {
-        const T v = base[r * inner];
-        const T next = acc + v;
-        carry += (fabs(acc) >= fabs(v)) ? (acc - next) + v : (v - next) + acc;
-        acc = next;
-      }
-      out[g] = acc + carry;
-    } else {
-      T acc = C::identity();
-      for (int64_t r = 0; r < reduced; ++r) acc = C::apply(acc, base[r * inner]);
-      out[g] = acc;
-    }
+  static constexpr int kBatch = 8;
+  __device__ static T identity_in() { return C::identity(); }
+  __device__ static T identity() { return C::identity(); }
+  __device__ static T fold(T acc, const T (&v)[kBatch]) {
+#pragma unroll
+    for (int j = 0; j < kBatch; ++j) acc = C::apply(acc, v[j]);
+    return acc;
   }
+  __device__ static T combine(T a, T b) { return C::apply(a, b); }
+  __device__ static T finish(T a) { return a; }
+};
+
+template <typename T>
+constexpr int vector_max() {
+  return sizeof(T) == 4 ? 4 : (sizeof(T) == 8 ? 2 : 1);
+}
+
+template <typename T, int OP>
+void run_cols(hp_ctx* ctx, const T* x, T* out, int64_t outer, int64_t reduced, int64_t inner) {
+  const int v_in = hps::vector_width(x, inner, sizeof(T));
+  const int v_acc = hps::vector_width(reinterpret_cast<const void*>(256), inner, sizeof(T));
+  const hps::Plan plan = hps::plan(outer, reduced, inner, v_in, v_acc, sizeof(T), ctx->compute_units);
+  void* buffers[2] = {nullptr, nullptr};
+  for (int i = 0; i < 2; ++i)
+    if (plan.bytes[i] > 0) buffers[i] = hp::scratch_alloc(ctx, plan.bytes[i]);
+  using Op = ColumnOp<T, OP>;
+  hps::execute<Op, Op, vector_max<T>(), vector_max<T>()>(ctx->stream, plan, x, out, outer, reduced, inner, buffers);
+  for (int i = 0; i < 2; ++i)
+    if (buffers[i]) hp::scratch_free(ctx, buffers[i]);
 }
 
 template <typename T, int OP>
 void run(hp_ctx* ctx, const T* x, T* out, int64_t outer, int64_t reduced, int64_t inner) {
-  if (inner > 1) {
-    int64_t grid = hp::ceil_div(outer * inner, kBlock);
-    if (grid > 65536 * 4) grid = 65536 * 4;
-    reduce_cols_kernel<T, OP><<<grid, kBlock, 0, ctx->stream>>>(x, out, outer, reduced, inner);
-    hp::check_launch("reduce_cols");
-    return;
-  }
+  if (inner > 1) return run_cols<T, OP>(ctx, x, out, outer, reduced, inner);
   const int64_t chunks = hp::ceil_div(reduced, kChunk);
   const int64_t grid = outer * chunks;
   hp::require(grid <= hp::kMaxGrid, "reduction too large for one launch");
