@@ -15,6 +15,7 @@ import argparse
 import ctypes
 import json
 import os
+import statistics
 import sys
 import time
 from pathlib import Path
@@ -122,6 +123,78 @@ def cpu_threads():
         return os.cpu_count() or 1
 
 
+def cpu_timed(fn, min_calls=7, min_seconds=0.0):
+    """The CPU baseline protocol: warm-up of at least 3 calls and 0.25 s, then
+    the median of at least ``min_calls`` timed calls (and ``min_seconds``)."""
+    t0, calls = time.perf_counter(), 0
+    while calls < 3 or time.perf_counter() - t0 < 0.25:
+        fn()
+        calls += 1
+    times, t1 = [], time.perf_counter()
+    while len(times) < min_calls or time.perf_counter() - t1 < min_seconds:
+        start = time.perf_counter()
+        fn()
+        times.append(time.perf_counter() - start)
+    return statistics.median(times), len(times)
+
+
+def blas_threads(count):
+    """Limit NumPy's BLAS to ``count`` threads inside a with-block."""
+    from threadpoolctl import threadpool_limits
+
+    return threadpool_limits(limits=count, user_api="blas")
+
+
+def cpu_blas_seconds(fn, min_seconds=0.0):
+    """Median seconds per call of a BLAS-backed ``fn`` at every core the
+    process may use and at 1 thread: (cores, seconds, calls, seconds_1, calls_1)."""
+    cores = cpu_threads()
+    with blas_threads(cores):
+        sec, calls = cpu_timed(fn, min_seconds=min_seconds)
+    with blas_threads(1):
+        sec1, calls1 = cpu_timed(fn)
+    return cores, sec, calls, sec1, calls1
+
+
+def cpu_blas(fn, work, unit, sample, min_seconds=0.0):
+    """A BLAS-backed CPU leg at every core the process may use and at 1 thread.
+    ``work`` is the algorithmic flop or byte count of one call of ``fn``."""
+    scale = 1e9
+    cores, sec, calls, sec1, calls1 = cpu_blas_seconds(fn, min_seconds)
+    return {
+        "value": round(work / sec / scale, 3),
+        "unit": unit,
+        "cores": cores,
+        "kind": "port",
+        "sample": f"{sample}; median of {calls} calls",
+        "one_thread": {"value": round(work / sec1 / scale, 3), "unit": unit, "cores": 1, "calls": calls1},
+    }
+
+
+def cpu_single(fn, work, unit, sample, scale=1e9):
+    """A single-threaded NumPy elementwise CPU leg (the norm and RNG restatements)."""
+    sec, calls = cpu_timed(fn)
+    return {
+        "value": round(work / sec / scale, 4),
+        "unit": unit,
+        "cores": 1,
+        "kind": "port",
+        "sample": f"{sample}; single-threaded NumPy; median of {calls} calls",
+    }
+
+
+def strict_json(value):
+    """Non-finite floats become strings, so the line is strict JSON (the
+    convention of reference benchmarks/numerical_metrics.py:13-18)."""
+    if isinstance(value, dict):
+        return {k: strict_json(v) for k, v in value.items()}
+    if isinstance(value, (list, tuple)):
+        return [strict_json(v) for v in value]
+    if isinstance(value, float) and not np.isfinite(value):
+        return str(value)
+    return value
+
+
 def bench_gemm(p, hip, steps, warmup):
     n = 8192
     rng = p.random.default_rng(3, backend=hip)
@@ -148,31 +221,25 @@ def bench_gemm(p, hip, steps, warmup):
 
 
 def cpu_gemm_baseline(p, gemm):
-    """np.matmul (the reference NumPy backend's path) on a row sample of the same product."""
+    """np.matmul (the reference NumPy backend's path) on a row sample of the
+    same product: about 10 s at every core, plus a 64-row sample at 1 thread."""
     from oracle import numpy_backend
 
     rows = int(os.environ.get("PACHO_BENCH_CPU_ROWS", "1024"))
     a = p.asnumpy(gemm["a"][:rows])
     b = p.asnumpy(gemm["b"])
-    numpy_backend.matmul(a[:64], b)  # warm the BLAS thread pool
-    reps, t0 = 0, time.perf_counter()
-    while reps < 3 or time.perf_counter() - t0 < 10.0:  # about 10 s of CPU work
-        numpy_backend.matmul(a, b)
-        reps += 1
-    seconds = (time.perf_counter() - t0) / reps
-    gflops = 2.0 * rows * 8192 * 8192 / seconds / 1e9
-    try:
-        from threadpoolctl import threadpool_info
-
-        threads = max((i.get("num_threads", 1) for i in threadpool_info() if i.get("user_api") == "blas"), default=1)
-    except Exception:  # noqa: BLE001
-        threads = cpu_threads()
+    cores = cpu_threads()
+    with blas_threads(cores):
+        sec, calls = cpu_timed(lambda: numpy_backend.matmul(a, b), min_seconds=10.0)
+    with blas_threads(1):
+        sec1, calls1 = cpu_timed(lambda: numpy_backend.matmul(a[:64], b))
     return {
-        "value": round(gflops, 2),
+        "value": round(2.0 * rows * 8192 * 8192 / sec / 1e9, 2),
         "unit": "GFLOP/s",
-        "cores": int(threads),
+        "cores": cores,
         "kind": "port",
-        "sample": f"np.matmul float32 A[:{rows}] @ B (8192x8192), {reps} reps (mean)",
+        "sample": f"np.matmul float32 A[:{rows}] @ B (8192x8192) at {cores} BLAS threads; median of {calls} calls",
+        "one_thread": {"value": round(2.0 * 64 * 8192 * 8192 / sec1 / 1e9, 2), "unit": "GFLOP/s", "cores": 1, "sample": "A[:64] @ B", "calls": calls1},
     }
 
 
@@ -251,30 +318,45 @@ def bench_extras(p, hip, only, skip_cpu):
     def want(name):
         return not only or name in only
 
+    def hbm(key, bytes_moved, ms, wall, traffic_key):
+        extra[key] = {
+            "value": round(bytes_moved / (ms * 1e-3) / 1e9, 1),
+            "unit": "GB/s",
+            "kernel_us": round(ms * 1e3, 2),
+            "wall_us": round(wall * 1e3, 2),
+            "roofline": roofline("hbm", bytes_moved, ms, _traffic(traffic_key)),
+        }
+
+    def mfma(key, flops, ms, traffic_key, bound="mfma"):
+        extra[key] = {
+            "value": round(flops / (ms * 1e-3) / 1e9, 1),
+            "unit": "GFLOP/s",
+            "kernel_ms": round(ms, 4),
+            "roofline": roofline(bound, flops, ms, _traffic(traffic_key)),
+        }
+
     if want("gemv"):
         n = 16384
         rng = p.random.default_rng(1, backend=hip)
         A = rng.uniform(-1, 1, (n, n), dtype="float32")
         x = rng.normal(0, 1, n, dtype="float32")
         ms, wall = timer.run(lambda: A @ x, 20)
-        bytes_moved = n * n * 4 + 2 * n * 4
-        extra["gemv_f32_16384"] = {
-            "value": round(bytes_moved / (ms * 1e-3) / 1e9, 1),
-            "unit": "GB/s",
-            "kernel_us": round(ms * 1e3, 2),
-            "wall_us": round(wall * 1e3, 2),
-            "roofline": roofline("hbm", bytes_moved, ms, _traffic("gemv")),
-        }
+        hbm("gemv_f32_16384", n * n * 4 + 2 * n * 4, ms, wall, "gemv")
         ms, wall = timer.run(lambda: p.dot(x, x), 50)
         extra["dot_f32_16384"] = {"value": round(ms * 1e3, 2), "unit": "us", "wall_us": round(wall * 1e3, 2)}
         if not skip_cpu:
-            host_a, host_x = p.asnumpy(A), p.asnumpy(x)
-            reps, t0 = 0, time.perf_counter()
-            while reps < 3 or time.perf_counter() - t0 < 3.0:
-                numpy_backend.matmul(host_a, host_x)
-                reps += 1
-            sec = (time.perf_counter() - t0) / reps
-            extra["gemv_f32_16384"]["cpu_baseline"] = {"value": round(bytes_moved / sec / 1e9, 2), "unit": "GB/s", "cores": cpu_threads(), "kind": "port"}
+            rows = 4096
+            host_a, host_x = p.asnumpy(A[:rows]), p.asnumpy(x)
+            extra["gemv_f32_16384"]["cpu_baseline"] = cpu_blas(
+                lambda: numpy_backend.matmul(host_a, host_x), rows * n * 4 + (rows + n) * 4, "GB/s",
+                f"np.matmul float32 A[:{rows}] @ x (n=16384)")
+            batch = 100  # calls per timing: one call is a few microseconds
+            cores, sec, calls, sec1, calls1 = cpu_blas_seconds(lambda: [numpy_backend.matmul(host_x, host_x) for _ in range(batch)])
+            extra["dot_f32_16384"]["cpu_baseline"] = {
+                "value": round(sec / batch * 1e6, 3), "unit": "us", "cores": cores, "kind": "port",
+                "sample": f"np.matmul(x, x), n=16384; median of {calls} timings of {batch} calls",
+                "one_thread": {"value": round(sec1 / batch * 1e6, 3), "unit": "us", "cores": 1, "calls": calls1},
+            }
             del host_a
         del A
     if want("norm"):
@@ -286,79 +368,115 @@ def bench_extras(p, hip, only, skip_cpu):
             x = p.where(signs, -mags, mags)
             del mags, signs
             ms, wall = timer.run(lambda: p.linalg.norm(x), 10)
-            bytes_moved = n * np.dtype(dtype).itemsize
             key = f"norm_flat_{dtype}_2^28"
-            extra[key] = {
-                "value": round(bytes_moved / (ms * 1e-3) / 1e9, 1),
-                "unit": "GB/s",
-                "kernel_us": round(ms * 1e3, 2),
-                "wall_us": round(wall * 1e3, 2),
-                "roofline": roofline("hbm", bytes_moved, ms, _traffic(f"norm_{dtype}")),
-            }
+            hbm(key, n * np.dtype(dtype).itemsize, ms, wall, f"norm_{dtype}")
             if not skip_cpu:
-                sample = p.asnumpy(x[: 1 << 24])
-                t0 = time.perf_counter()
-                numpy_backend.norm(sample)
-                sec = time.perf_counter() - t0
-                extra[key]["cpu_baseline"] = {"value": round(sample.nbytes / sec / 1e9, 2), "unit": "GB/s", "cores": 1, "kind": "port", "sample": "two-pass NumPy norm of 2^24 elements"}
+                sample = p.asnumpy(x[: 1 << 22])
+                extra[key]["cpu_baseline"] = cpu_single(
+                    lambda: numpy_backend.norm(sample), sample.nbytes, "GB/s", f"two-pass NumPy norm of 2^22 {dtype}")
             del x
         rows = p.random.default_rng(2, backend=hip).uniform(-1, 1, (65536, 4096), dtype="float32")
         ms, wall = timer.run(lambda: p.linalg.norm(rows, axis=1), 10)
-        bytes_moved = 65536 * 4096 * 4 + 65536 * 4
-        extra["norm_rows_f32_65536x4096"] = {
-            "value": round(bytes_moved / (ms * 1e-3) / 1e9, 1),
-            "unit": "GB/s",
-            "kernel_us": round(ms * 1e3, 2),
-            "roofline": roofline("hbm", bytes_moved, ms, _traffic("norm_rows")),
-        }
+        hbm("norm_rows_f32_65536x4096", 65536 * 4096 * 4 + 65536 * 4, ms, wall, "norm_rows")
+        if not skip_cpu:
+            sample = p.asnumpy(rows[:1024])
+            extra["norm_rows_f32_65536x4096"]["cpu_baseline"] = cpu_single(
+                lambda: numpy_backend.norm(sample, axis=1), sample.nbytes + 1024 * 4, "GB/s", "two-pass NumPy norm, axis=1, of 1024x4096 float32")
         del rows
+    if want("strided"):
+        rows, cols = 262144, 1024
+        data = p.random.default_rng(3, backend=hip).uniform(-1, 1, (rows, cols), dtype="float32")
+        bytes_moved = rows * cols * 4 + cols * 4
+        sample = p.asnumpy(data[:16384]) if not skip_cpu else None
+        for name, fn, host_fn in (
+            ("sum", lambda: p.sum(data, axis=0), lambda: np.sum(sample, axis=0)),
+            ("max", lambda: p.max(data, axis=0), lambda: np.max(sample, axis=0)),
+            ("norm", lambda: p.linalg.norm(data, axis=0), lambda: numpy_backend.norm(sample, axis=0)),
+        ):
+            ms, wall = timer.run(fn, 10)
+            key = f"{name}_axis0_f32_262144x1024"
+            hbm(key, bytes_moved, ms, wall, f"strided_{name}")
+            if sample is not None:
+                extra[key]["cpu_baseline"] = cpu_single(
+                    host_fn, sample.nbytes + cols * 4, "GB/s", f"NumPy {name} over axis 0 of a 16384x1024 float32 sample")
+        del data, sample
     if want("rng"):
         n = 1 << 28
         for dist in ("uniform", "normal", "exponential"):
             rng = p.random.default_rng(42, backend=hip)
             ms, wall = timer.run(lambda: getattr(rng, dist)(size=n, dtype="float32"), 100)
-            bytes_moved = n * 4
-            extra[f"rng_{dist}_f32_2^28"] = {
+            key = f"rng_{dist}_f32_2^28"
+            extra[key] = {
                 "value": round(n / (ms * 1e-3) / 1e9, 2),
                 "unit": "Gsample/s",
                 "kernel_us": round(ms * 1e3, 2),
-                "roofline": roofline("hbm", bytes_moved, ms, _traffic(f"rng_{dist}")),
+                "roofline": roofline("hbm", n * 4, ms, _traffic(f"rng_{dist}")),
                 "valu_roofline": _valu(f"rng_{dist}", n, ms),
                 "alu_bound_note": "vector-ALU issue bound: one Philox4x32-10 block per sample = ~17 v_mad_u64_u32 + ~17 three-input XORs (v_bitop3_b32) per sample",
             }
-        if not skip_cpu:
-            count = 1 << 22
-            t0 = time.perf_counter()
-            numpy_backend.random("normal", "float32", (count,), 42)
-            sec = time.perf_counter() - t0
-            extra["rng_normal_f32_2^28"]["cpu_baseline"] = {"value": round(count / sec / 1e9, 4), "unit": "Gsample/s", "cores": 1, "kind": "port", "sample": "NumPy Philox normal, 2^22 samples"}
+            if not skip_cpu:
+                count = 1 << 20
+                extra[key]["cpu_baseline"] = cpu_single(
+                    lambda: numpy_backend.random(dist, "float32", (count,), 42), count, "Gsample/s",
+                    f"NumPy Philox {dist} float32, 2^20 samples")
     if want("gemm_f64"):
         n = 4096
         rng = p.random.default_rng(3, backend=hip)
         a = rng.uniform(-1, 1, (n, n), dtype="float64")
         b = rng.uniform(-1, 1, (n, n), dtype="float64")
         ms, wall = timer.run(lambda: a @ b, 5)
-        flops = 2.0 * n**3
-        extra["gemm_f64_4096"] = {"value": round(flops / (ms * 1e-3) / 1e9, 1), "unit": "GFLOP/s", "kernel_ms": round(ms, 4), "roofline": roofline("mfma_fp64", flops, ms, _traffic("gemm_f64"))}
+        mfma("gemm_f64_4096", 2.0 * n**3, ms, "gemm_f64", bound="mfma_fp64")
+        if not skip_cpu:
+            ha, hb = p.asnumpy(a[:512]), p.asnumpy(b)
+            extra["gemm_f64_4096"]["cpu_baseline"] = cpu_blas(
+                lambda: numpy_backend.matmul(ha, hb), 2.0 * 512 * n * n, "GFLOP/s", "np.matmul float64 A[:512] @ B (4096x4096)")
         del a, b
     if want("gemm_padded"):
         m, k, n = 4097, 3001, 2049
         rng = p.random.default_rng(3, backend=hip)
         a = rng.uniform(-1, 1, (m, k), dtype="float32")
         b = rng.uniform(-1, 1, (k, n), dtype="float32")
-        ms, wall = timer.run(lambda: p.matmul(a, b, padding=True), 10)
         flops = 2.0 * m * n * k
-        extra["gemm_f32_4097x3001x2049_padded"] = {"value": round(flops / (ms * 1e-3) / 1e9, 1), "unit": "GFLOP/s", "kernel_ms": round(ms, 4), "roofline": roofline("mfma", flops, ms)}
+        ms, wall = timer.run(lambda: p.matmul(a, b, padding=True), 10)
+        mfma("gemm_f32_4097x3001x2049_padded", flops, ms, "gemm_padded")
         ms, wall = timer.run(lambda: a @ b, 10)
-        extra["gemm_f32_4097x3001x2049_unpadded"] = {"value": round(flops / (ms * 1e-3) / 1e9, 1), "unit": "GFLOP/s", "kernel_ms": round(ms, 4), "roofline": roofline("mfma", flops, ms)}
+        mfma("gemm_f32_4097x3001x2049_unpadded", flops, ms, "gemm_unpadded")
+        if not skip_cpu:
+            ha, hb = p.asnumpy(a[:1024]), p.asnumpy(b)
+            leg = cpu_blas(lambda: numpy_backend.matmul(ha, hb), 2.0 * 1024 * n * k, "GFLOP/s", "np.matmul float32 A[:1024] @ B (3001x2049)")
+            extra["gemm_f32_4097x3001x2049_padded"]["cpu_baseline"] = leg
+            extra["gemm_f32_4097x3001x2049_unpadded"]["cpu_baseline"] = leg
         del a, b
     if want("gemm_batched"):
         rng = p.random.default_rng(3, backend=hip)
         a = rng.uniform(-1, 1, (64, 512, 1024), dtype="float32")
         b = rng.uniform(-1, 1, (1024, 768), dtype="float32")
         ms, wall = timer.run(lambda: a @ b, 10)
-        flops = 2.0 * 64 * 512 * 768 * 1024
-        extra["gemm_f32_batched_64x512x1024x768"] = {"value": round(flops / (ms * 1e-3) / 1e9, 1), "unit": "GFLOP/s", "kernel_ms": round(ms, 4), "roofline": roofline("mfma", flops, ms)}
+        mfma("gemm_f32_batched_64x512x1024x768", 2.0 * 64 * 512 * 768 * 1024, ms, "gemm_batched")
+        if not skip_cpu:
+            ha, hb = p.asnumpy(a[:8]), p.asnumpy(b)
+            extra["gemm_f32_batched_64x512x1024x768"]["cpu_baseline"] = cpu_blas(
+                lambda: numpy_backend.matmul(ha, hb), 2.0 * 8 * 512 * 768 * 1024, "GFLOP/s", "np.matmul float32 A[:8] @ B, batch of 8")
+        del a, b
+    if want("gemm_small"):
+        # Config 1's shape: 1024^3 float32, seed 0 host inputs; the GPU product
+        # beside the reference CPU path itself (NumPy's BLAS) and its error.
+        gen = np.random.default_rng(0)
+        ha = gen.uniform(-1, 1, (1024, 1024)).astype(np.float32)
+        hb = gen.uniform(-1, 1, (1024, 1024)).astype(np.float32)
+        a, b = p.asarray(ha, backend=hip), p.asarray(hb, backend=hip)
+        ms, wall = timer.run(lambda: a @ b, 50)
+        flops = 2.0 * 1024**3
+        mfma("gemm_f32_1024", flops, ms, "gemm_1024")
+        exact64 = ha.astype(np.float64) @ hb.astype(np.float64)
+        got = p.asnumpy(a @ b).astype(np.float64)
+        extra["gemm_f32_1024"]["rel_l2_vs_float64"] = float(np.linalg.norm(got - exact64) / np.linalg.norm(exact64))
+        if not skip_cpu:
+            leg = cpu_blas(lambda: numpy_backend.matmul(ha, hb), flops, "GFLOP/s", "config 1: np.matmul float32 1024x1024x1024, seed 0")
+            cpu_c = numpy_backend.matmul(ha, hb).astype(np.float64)
+            leg["rel_l2_vs_float64"] = float(np.linalg.norm(cpu_c - exact64) / np.linalg.norm(exact64))
+            extra["gemm_f32_1024"]["cpu_baseline"] = leg
+            extra["config1_cpu_gemm_f32_1024"] = dict(leg, note="BASELINE config 1 (the reference NumPy backend path), measured on this host")
         del a, b
     if only and "copy" in only:
         # Calibration for rocprofv3 --pmc: a plain 1 GiB float32 copy
@@ -386,14 +504,22 @@ def bench_extras(p, hip, only, skip_cpu):
 
         ms, wall = timer.run(lambda: mlp(x, *params), 5)
         flops = 2.0 * 8192 * (4096 * 4096 * 2 + 4096 * 1024)
-        extra["mlp_forward_f32_8192x4096"] = {
-            "value": round(flops / (ms * 1e-3) / 1e9, 1),
-            "unit": "GFLOP/s",
-            "kernel_ms": round(ms, 4),
-            "wall_ms": round(wall, 4),
-            "steps": [s["kind"] for s in mlp.explain(x, *params)["steps"]],
-            "roofline": roofline("mfma", flops, ms),
-        }
+        mfma("mlp_forward_f32_8192x4096", flops, ms, "mlp")
+        extra["mlp_forward_f32_8192x4096"]["wall_ms"] = round(wall, 4)
+        extra["mlp_forward_f32_8192x4096"]["steps"] = [s["kind"] for s in mlp.explain(x, *params)["steps"]]
+        if not skip_cpu:
+            rows = 256
+            hx = p.asnumpy(x[:rows])
+            hosts = [p.asnumpy(v) for v in params]
+
+            def forward():
+                h = hx
+                for w, bias in zip(hosts[0::2], hosts[1::2]):
+                    h = np.tanh(numpy_backend.matmul(h, w) + bias)
+                return h.mean(axis=1)
+
+            extra["mlp_forward_f32_8192x4096"]["cpu_baseline"] = cpu_blas(
+                forward, flops * rows / 8192, "GFLOP/s", f"NumPy forward of {rows} rows (np.matmul + np.tanh + mean)")
     if want("vendor"):
         extra.update(vendor_gemm())
     return extra
@@ -406,7 +532,7 @@ def main(argv=None):
     parser.add_argument("--warmup", type=int, default=15)
     parser.add_argument("--skip-cpu", action="store_true", help="omit the CPU baselines")
     parser.add_argument("--vendor-child", action="store_true", help=argparse.SUPPRESS)
-    parser.add_argument("--only", default="", help="comma-separated extras to run (gemv,norm,rng,gemm_f64,gemm_padded,gemm_batched,mlp,vendor; copy = PMC calibration, only when named); 'none' for the headline only")
+    parser.add_argument("--only", default="", help="comma-separated extras to run (gemv,norm,strided,rng,gemm_f64,gemm_padded,gemm_batched,gemm_small,mlp,vendor; copy = PMC calibration, only when named); 'none' for the headline only")
     args = parser.parse_args(argv)
     if args.vendor_child:
         print(json.dumps(vendor_gemm_child()), flush=True)
@@ -456,7 +582,7 @@ def main(argv=None):
         "kernel_ms_per_step": round(gemm["kernel_ms"], 4),
         "extra": extra,
     }
-    print(json.dumps(result), flush=True)
+    print(json.dumps(strict_json(result)), flush=True)
     return 0
 
 

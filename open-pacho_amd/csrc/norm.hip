@@ -310,7 +310,9 @@ template <typename T>
 hps::Plan plan_cols(hp_ctx* ctx, const T* x, int64_t outer, int64_t reduced, int64_t inner) {
   const int v_in = hps::vector_width(x, inner, sizeof(T));
   const int v_acc = hps::vector_width(reinterpret_cast<const void*>(256), inner, sizeof(Pair<T>));
-  return hps::plan(outer, reduced, inner, v_in, v_acc, sizeof(Pair<T>), ctx->compute_units);
+  // 2 workgroups per compute unit: 1 GiB float32 axis 0 at 68% of HBM against
+  // 64% at 4 (one MI355X).
+  return hps::plan(outer, reduced, inner, v_in, v_acc, sizeof(Pair<T>), ctx->compute_units, 2);
 }
 
 template <typename T>

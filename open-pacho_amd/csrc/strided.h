@@ -176,9 +176,11 @@ struct Plan {
 // gets at least kFirstRows rows to keep loads in flight; merge passes read
 // small partial arrays and take long chunks, so that few passes remain.
 constexpr int64_t kFirstRows = 16;
-constexpr int64_t kMergeRows = 64;
-// Workgroups the first pass aims for (several per compute unit).
-constexpr int64_t kGroupsPerCU = 8;
+constexpr int64_t kMergeRows = 32;
+// Workgroups the merge passes aim for per compute unit; the first pass takes
+// its own figure from the caller (the op's fold cost decides: a cheap fold
+// runs best with few long chunks, an expensive one with more, shorter ones).
+constexpr int64_t kGroupsPerCU = 4;
 // The first pass's partial array is kept below this size by using fewer,
 // longer chunks; this also bounds the static workspace of allocation-free
 // callers.
@@ -214,7 +216,7 @@ inline Pass plan_pass(int64_t outer, int64_t reduced, int64_t inner, int V, int6
 // sizes of the input and of the accumulator; V_in / V_acc: vector widths the
 // first and the merge passes may use (1 if the rows are not 16-byte aligned).
 inline Plan plan(int64_t outer, int64_t reduced, int64_t inner, int V_in, int V_acc, int64_t acc_bytes,
-                 int64_t compute_units) {
+                 int64_t compute_units, int64_t first_groups_per_cu) {
   Plan plan;
   const int64_t cw0 = hp::ceil_div(inner, V_in) < kThreads ? hp::ceil_div(inner, V_in) : kThreads;
   if (reduced * 2 < kThreads / cw0) {
@@ -224,8 +226,9 @@ inline Plan plan(int64_t outer, int64_t reduced, int64_t inner, int V_in, int V_
   int64_t rows = reduced;
   for (;;) {
     const bool first = plan.count == 0;
-    Pass p = plan_pass(outer, rows, inner, first ? V_in : V_acc, compute_units * kGroupsPerCU,
-                       first ? kFirstRows : kMergeRows, acc_bytes, first);
+    Pass p = plan_pass(outer, rows, inner, first ? V_in : V_acc,
+                       compute_units * (first ? first_groups_per_cu : kGroupsPerCU), first ? kFirstRows : kMergeRows,
+                       acc_bytes, first);
     hp::require(plan.count < 12, "strided reduction needs too many passes");
     hp::require(outer * p.col_blocks * p.chunks <= hp::kMaxGrid, "strided reduction too large for one launch");
     plan.passes[plan.count] = p;

@@ -132,8 +132,8 @@ def _merge(s, t, v, w):
     return s, t
 
 
-def norm_pair_merge(x):
-    """Norm of a 1-D float array following the reference GPU kernel's passes.
+def norm_pair_state(x):
+    """The (scale, ssq) pair the reference GPU kernel's last pass merges to.
 
     Vectorised across the 4096-term chunks of a pass: lanes past the end of a
     chunk hold zeros, which the merge treats as absent terms (v > 0 fails).
@@ -141,7 +141,7 @@ def norm_pair_merge(x):
     x = np.asarray(x)
     dt = x.dtype
     if x.shape[0] == 0:
-        return dt.type(0)
+        return dt.type(0), dt.type(0)
     values, weights = np.abs(x), np.ones_like(x)
     while True:
         n = values.shape[0]
@@ -161,6 +161,17 @@ def norm_pair_merge(x):
             s[:, :half], t[:, :half] = s_lo, t_lo
             half //= 2
         if chunks == 1:
-            with np.errstate(all="ignore"):
-                return dt.type(s[0, 0] * np.sqrt(t[0, 0]))
+            return s[0, 0], t[0, 0]
         values, weights = s[:, 0].copy(), t[:, 0].copy()
+
+
+def norm_pair_merge(x):
+    """Norm of a 1-D float array following the reference GPU kernel's passes:
+    s * sqrt(t) of norm_pair_state (0 for an empty array)."""
+    x = np.asarray(x)
+    dt = x.dtype
+    if x.shape[0] == 0:
+        return dt.type(0)
+    s, t = norm_pair_state(x)
+    with np.errstate(all="ignore"):
+        return dt.type(s * np.sqrt(t))

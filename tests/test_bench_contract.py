@@ -66,3 +66,30 @@ def test_warm_up_runs_the_minimum_calls_and_the_minimum_time(monkeypatch):
     calls.clear()
     bench.warm(lambda: calls.append(1), lambda: None, 5)
     assert len(calls) == 5
+
+
+def test_cpu_baseline_protocol_warms_then_takes_the_median_of_seven():
+    calls = []
+    start = bench.time.perf_counter()
+    seconds, timed = bench.cpu_timed(lambda: calls.append(bench.time.perf_counter()))
+    elapsed = bench.time.perf_counter() - start
+    assert timed >= 7 and len(calls) >= timed + 3
+    warm_calls = [t for t in calls if t - start < 0.25]
+    assert len(warm_calls) >= 3 and elapsed >= 0.25
+    assert seconds >= 0
+
+
+def test_cpu_blas_legs_report_affinity_cores_and_one_thread():
+    import numpy as np
+
+    a = np.ones((64, 64), np.float32)
+    leg = bench.cpu_blas(lambda: a @ a, 2.0 * 64**3, "GFLOP/s", "64^3")
+    assert leg["cores"] == bench.cpu_threads() and leg["kind"] == "port"
+    assert leg["one_thread"]["cores"] == 1 and leg["one_thread"]["value"] > 0
+    assert "median of" in leg["sample"]
+
+
+def test_strict_json_writes_non_finite_numbers_as_strings():
+    line = bench.strict_json({"a": float("inf"), "b": [float("nan"), 1.5], "c": {"d": -float("inf")}, "e": 2})
+    assert line == {"a": "inf", "b": ["nan", 1.5], "c": {"d": "-inf"}, "e": 2}
+    json.loads(json.dumps(line, allow_nan=False))

@@ -6,6 +6,8 @@ with the hip error bounded by 2x the error of the reference cooperative
 kernel's arithmetic order (oracle.kernels.gemv_lanes).
 """
 
+from fractions import Fraction
+
 import numpy as np
 import pytest
 
@@ -129,6 +131,19 @@ def test_residual_matches_eager_rounding_bit_for_bit(hip, dtype, shape, monkeypa
     actual = p.asnumpy(ndarray._wrap(out, b.shape, b.dtype, hip))
     np.testing.assert_array_equal(actual, expected)
     assert out is not b._data
+    # The same bits as NumPy's subtraction of the downloaded product: one
+    # rounding of the product, then one of the difference.
+    np.testing.assert_array_equal(actual, host_b - product)
+    # Against the exact residual b - A x of the same inputs: the product's
+    # error (k terms, each rounding at most once per add) plus one rounding.
+    if shape[0] and shape[1]:
+        host_a, host_x = p.asnumpy(a), p.asnumpy(x)
+        eps = float(np.finfo(dtype).eps)
+        for r in range(shape[0]):
+            exact_r = Fraction(float(host_b[r])) - exact.exact_dot(host_a[r], host_x)
+            scale = float(exact.exact_dot(np.abs(host_a[r]), np.abs(host_x)))
+            bound = (shape[1] + 1) * eps * scale + eps * abs(float(exact_r))
+            assert abs(float(Fraction(float(actual[r])) - exact_r)) <= bound, r
 
 
 @pytest.mark.parametrize("dtype", [np.float32, np.float64])

@@ -190,3 +190,109 @@ def test_padding_closed_form_matches_reference_worked_values():
     for a, b in [((31, 16), (16, 32)), ((0, 32), (32, 96))]:
         assert padding.plan(a, b) is None
     assert padding.plan((33, 17), (17, 65), "float64") is None
+
+
+# ---- brute-force scalar restatements of the reference kernels' loops -------------------
+# These walk lanes, chunks and tree steps one scalar at a time, in the order
+# of reference _norm.py:62-118 (with _merge :28-36) and _cuda.py:466-485, with
+# NumPy scalars of the kernel's dtype (every operation rounds once). The
+# vectorised oracles must reproduce them bit for bit.
+
+
+def _scalar_merge(dt, s, t, v, w):
+    if np.isnan(s) or np.isnan(v):
+        s = dt(s + v)
+        return s, s
+    if np.isinf(v):
+        return v, dt(1)
+    if not np.isinf(s) and v > dt(0):
+        if s < v:
+            z = dt(s / v)
+            return v, dt(w + dt(dt(t * z) * z))
+        z = dt(v / s)
+        return s, dt(t + dt(dt(w * z) * z))
+    return s, t
+
+
+def _scalar_norm_kernel(values):
+    dt = values.dtype.type
+    current = [(abs(v), dt(1)) for v in values]
+    while True:
+        reduced = len(current)
+        chunks = (reduced + 4095) // 4096
+        out = []
+        for chunk in range(chunks):
+            scales, sums = [dt(0)] * 128, [dt(0)] * 128
+            for lane in range(128):
+                s, t = dt(0), dt(0)
+                for j in range(lane, min(4096, reduced - chunk * 4096), 128):
+                    v, w = current[chunk * 4096 + j]
+                    s, t = _scalar_merge(dt, s, t, v, w)
+                scales[lane], sums[lane] = s, t
+            step = 64
+            while step:
+                for lane in range(step):
+                    scales[lane], sums[lane] = _scalar_merge(dt, scales[lane], sums[lane], scales[lane + step], sums[lane + step])
+                step //= 2
+            out.append((scales[0], sums[0]))
+        if chunks == 1:
+            return out[0]
+        current = out
+
+
+def _scalar_reduce_kernel(values):
+    dt = values.dtype.type
+    current = list(values)
+    while True:
+        reduced = len(current)
+        chunks = (reduced + 4095) // 4096
+        partial = []
+        for chunk in range(chunks):
+            sums = []
+            for lane in range(128):
+                acc = dt(0)
+                for r in range(chunk * 4096 + lane, min((chunk + 1) * 4096, reduced), 128):
+                    acc = dt(acc + current[r])
+                sums.append(acc)
+            step = 64
+            while step:
+                for lane in range(step):
+                    sums[lane] = dt(sums[lane] + sums[lane + step])
+                step //= 2
+            partial.append(sums[0])
+        if chunks == 1:
+            return partial[0]
+        current = partial
+
+
+@pytest.mark.parametrize("dtype", [np.float32, np.float64])
+def test_pair_merge_matches_the_scalar_kernel_loop(dtype):
+    rng = np.random.default_rng(31)
+    cases = [
+        rng.uniform(-1, 1, 300),
+        10.0 ** rng.uniform(-30, 30, 300) * rng.choice([-1, 1], 300),
+        np.concatenate([np.zeros(40), rng.normal(size=200), [0.0] * 7]),
+        rng.normal(size=2 * 4096 + 77),  # two chunks, then a second pass over the pairs
+        10.0 ** rng.uniform(-20, 20, 3 * 4096 + 1),
+    ]
+    for values in cases:
+        values = values.astype(dtype)
+        want_s, want_t = _scalar_norm_kernel(values)
+        got_s, got_t = kernels.norm_pair_state(values)
+        assert got_s.dtype == dtype and got_t.dtype == dtype
+        assert (got_s.tobytes(), got_t.tobytes()) == (dtype(want_s).tobytes(), dtype(want_t).tobytes())
+        with np.errstate(all="ignore"):
+            assert kernels.norm_pair_merge(values).tobytes() == dtype(want_s * dtype(np.sqrt(want_t))).tobytes()
+    special = np.ones(300, dtype)
+    special[17], special[250] = np.inf, np.nan
+    assert np.isnan(kernels.norm_pair_merge(special)) and np.isnan(_scalar_norm_kernel(special)[0])
+
+
+@pytest.mark.parametrize("dtype", [np.float32, np.float64])
+def test_reduce_lanes_matches_the_scalar_kernel_loop(dtype):
+    rng = np.random.default_rng(32)
+    for n in (1, 127, 300, 4096, 4097, 2 * 4096 + 300, 3 * 4096 * 2 + 5):
+        values = (rng.normal(size=n) * 10.0 ** rng.uniform(-3, 3, n)).astype(dtype)
+        want = _scalar_reduce_kernel(values)
+        got = kernels.reduce_lanes(values)
+        assert np.asarray(got).tobytes() == dtype(want).tobytes(), n
