@@ -8,7 +8,12 @@ Generator contract (reference random.py:42-135): a 64-bit seed; the backend
 is bound once at construction; calls are serialised and each reserves the
 counter range [counter, counter + count) before dispatch, so a failed or
 uncertain dispatch burns its range instead of reusing it; empty calls consume
-nothing; parameter domains are validated before rounding to the output dtype.
+nothing; parameter domains are validated before rounding to the output dtype
+and again after it.
+
+Layout of this module: a table of distributions (which raw and rounded
+parameter checks each one needs), a counter-range object that owns the
+reservation rule, and the Generator that resolves a request against both.
 """
 
 import operator
@@ -24,26 +29,90 @@ from .backends import get_backend
 
 __all__ = ["Generator", "default_rng"]
 
-_COUNTER_SPACE = 2**64
-_MAX_COUNT = 2**31 - 1
+_SEED_LIMIT = 1 << 64  # seeds and counters are 64-bit words
+_COUNT_LIMIT = (1 << 31) - 1  # largest output a backend indexes
+_FLOATS = frozenset((np.dtype(np.float32), np.dtype(np.float64)))
 
 
-def _reject_capture():
-    if getattr(get_backend(), "_is_tracing", False):
+def _tracing(backend):
+    return bool(getattr(backend, "_is_tracing", False))
+
+
+def _refuse_while_tracing(backend=None):
+    if _tracing(get_backend() if backend is None else backend):
         raise NotImplementedError("Random generation is not captured; pass generated arrays as arguments")
 
 
-def _rounded(value, dtype, label):
+# ---- parameter checks ---------------------------------------------------------
+# Each distribution names one check on the caller's values (so that a tiny
+# negative scale cannot round to a valid -0.0, nor inverted bounds to equal
+# ones) and one on the values rounded to the output dtype.
+
+
+def _accept(first, second):
+    return None
+
+
+def _scale_not_negative(_, scale):
+    if isinstance(scale, Real) and scale < 0:
+        raise ValueError("scale must be nonnegative")
+
+
+def _bounds_in_order(low, high):
+    if isinstance(low, Real) and isinstance(high, Real) and high < low:
+        raise ValueError("uniform requires high >= low")
+
+
+def _width_finite(low, high):
+    with np.errstate(over="ignore"):
+        width = high - low
+    if high < low or not np.isfinite(width):
+        raise ValueError("uniform requires high >= low and finite high-low in output dtype")
+
+
+_DISTRIBUTIONS = {
+    # name: (check of the given values, check of the rounded values)
+    "random": (_accept, _accept),
+    "uniform": (_bounds_in_order, _width_finite),
+    "normal": (_scale_not_negative, _scale_not_negative),
+    "exponential": (_scale_not_negative, _scale_not_negative),
+}
+
+
+def _in_dtype(value, dtype, role):
+    """The parameter as a finite scalar of the output dtype."""
     if not isinstance(value, Real):
-        raise TypeError(f"{label} must be a real scalar")
+        raise TypeError(f"{role} must be a real scalar")
+    problem = f"{role} must be finite and representable in {dtype}"
     try:
         with np.errstate(over="ignore", invalid="ignore"):
-            converted = dtype.type(value)
+            rounded = dtype.type(value)
     except OverflowError as exc:
-        raise ValueError(f"{label} must be finite and representable in {dtype}") from exc
-    if not np.isfinite(converted):
-        raise ValueError(f"{label} must be finite and representable in {dtype}")
-    return converted
+        raise ValueError(problem) from exc
+    if np.isfinite(rounded):
+        return rounded
+    raise ValueError(problem)
+
+
+class _CounterRange:
+    """The unused part [next, 2**64) of one seed's counter space.
+
+    take(count) hands out the next `count` counters and advances at once, so
+    a range is never handed out twice, whatever happens to the dispatch that
+    uses it.
+    """
+
+    __slots__ = ("next",)
+
+    def __init__(self):
+        self.next = 0
+
+    def take(self, count):
+        if count > _SEED_LIMIT - self.next:
+            raise OverflowError("Philox stream exhausted; create a generator with a new seed")
+        first = self.next
+        self.next = first + count
+        return first
 
 
 class Generator:
@@ -54,73 +123,80 @@ class Generator:
     """
 
     def __init__(self, seed=None, *, backend=None):
-        _reject_capture()
-        if seed is None:
-            seed = secrets.randbits(64)
+        _refuse_while_tracing()
+        self._seed = self._checked_seed(secrets.randbits(64) if seed is None else seed)
+        self._backend = get_backend(backend)
+        if _tracing(self._backend):
+            raise NotImplementedError("Random generation is not captured")
+        self._range = _CounterRange()
+        self._lock = Lock()
+
+    @staticmethod
+    def _checked_seed(seed):
         if isinstance(seed, (bool, np.bool_)):
             raise TypeError("seed must be an integer, not bool")
         seed = operator.index(seed)
-        if not 0 <= seed < _COUNTER_SPACE:
+        if seed < 0 or seed >= _SEED_LIMIT:
             raise ValueError("seed must be in [0, 2**64)")
-        self._backend = get_backend(backend)
-        if getattr(self._backend, "_is_tracing", False):
-            raise NotImplementedError("Random generation is not captured")
-        self._seed = seed
-        self._counter = 0
-        self._lock = Lock()
+        return seed
+
+    # The position of the stream (the next unused counter). Tests and tools
+    # move it to reach counter-carry cases.
+    @property
+    def _counter(self):
+        return self._range.next
+
+    @_counter.setter
+    def _counter(self, value):
+        self._range.next = operator.index(value)
 
     def random(self, size=None, dtype=np.float64):
         """Uniform samples in [0, 1); size=None returns a resident 0-D array."""
-        return self._generate("random", size, dtype, 0, 1)
+        return self._draw("random", size, dtype, 0, 1)
 
     def uniform(self, low=0.0, high=1.0, size=None, *, dtype=np.float64):
         """Uniform [low, high), or low when equal; bounds rounded to the output dtype."""
-        return self._generate("uniform", size, dtype, low, high)
+        return self._draw("uniform", size, dtype, low, high)
 
     def normal(self, loc=0.0, scale=1.0, size=None, *, dtype=np.float64):
         """Normal samples (Box-Muller); scalar location and nonnegative scale."""
-        return self._generate("normal", size, dtype, loc, scale)
+        return self._draw("normal", size, dtype, loc, scale)
 
     def exponential(self, scale=1.0, size=None, *, dtype=np.float64):
         """Exponential samples with nonnegative scalar scale (the mean)."""
-        return self._generate("exponential", size, dtype, 0, scale)
+        return self._draw("exponential", size, dtype, 0, scale)
 
-    def _generate(self, distribution, size, dtype, first, second):
-        _reject_capture()
+    def _output(self, size, dtype):
         dtype = np.dtype(dtype)
-        if dtype not in (np.dtype("float32"), np.dtype("float64")):
+        if dtype not in _FLOATS:
             raise TypeError("Random generation requires float32 or float64")
         self._backend.validate_dtype(dtype)
         shape = () if size is None else _shape(size)
-        count = prod(shape)
-        if count > _MAX_COUNT or any(d > np.iinfo(np.intp).max for d in shape):
+        if prod(shape) > _COUNT_LIMIT or max(shape, default=0) > np.iinfo(np.intp).max:
             raise ValueError("Random output exceeds indexing limits")
-        # Domain checks happen before rounding: a tiny negative scale must not
-        # become -0.0, nor inverted bounds become equal after rounding.
-        if distribution in ("normal", "exponential") and isinstance(second, Real) and second < 0:
-            raise ValueError("scale must be nonnegative")
-        if distribution == "uniform" and isinstance(first, Real) and isinstance(second, Real) and second < first:
-            raise ValueError("uniform requires high >= low")
-        first = _rounded(first, dtype, "first parameter")
-        second = _rounded(second, dtype, "second parameter")
-        if distribution == "uniform":
-            with np.errstate(over="ignore"):
-                width = second - first
-            if second < first or not np.isfinite(width):
-                raise ValueError("uniform requires high >= low and finite high-low in output dtype")
-        elif distribution in ("normal", "exponential") and second < 0:
-            raise ValueError("scale must be nonnegative")
+        return shape, dtype
+
+    def _kernel(self, distribution, dtype):
+        """The backend's generator entry point, if it offers this distribution."""
         generate = getattr(self._backend, "random_data", None)
         if generate is None:
             raise NotImplementedError("This backend does not implement random generation")
-        supported = getattr(self._backend, "random_distributions", lambda _dtype: ())
-        if distribution not in supported(dtype):
+        offered = getattr(self._backend, "random_distributions", None)
+        if offered is None or distribution not in offered(dtype):
             raise NotImplementedError(f"{self._backend.name} does not support {distribution} with {dtype}")
+        return generate
+
+    def _draw(self, distribution, size, dtype, first, second):
+        _refuse_while_tracing()
+        shape, dtype = self._output(size, dtype)
+        given, rounded = _DISTRIBUTIONS[distribution]
+        given(first, second)
+        first = _in_dtype(first, dtype, "first parameter")
+        second = _in_dtype(second, dtype, "second parameter")
+        rounded(first, second)
+        generate = self._kernel(distribution, dtype)
         with self._lock:
-            if self._counter + count > _COUNTER_SPACE:
-                raise OverflowError("Philox stream exhausted; create a generator with a new seed")
-            start = self._counter
-            self._counter = start + count  # reserved before dispatch
+            start = self._range.take(prod(shape))
             data = generate(shape, dtype, distribution, self._seed, start, first, second)
         return ndarray._wrap(data, shape, dtype, self._backend)
 
