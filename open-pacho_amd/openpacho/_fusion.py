@@ -4,10 +4,18 @@ While a function is captured, the default backend is a TraceBackend: every
 array operation records an Expression node instead of running. Node fields
 (``op``, ``inputs``, ``value``, ``resolved``, ``attrs``, ``shape``, ``dtype``)
 are the lowering protocol's view of the graph (reference _fusion.py:86-253).
-Host scalars passed as arguments become ScalarExpression values that are
+Host scalars passed as arguments become ScalarExpression terms that are
 re-evaluated from the bindings of every call, so cached plans never freeze
 them. Host observations, synchronisation, uninitialised arrays and random
 generation are rejected during capture.
+
+Two kinds of captured value live here:
+- ScalarExpression, a tree of host arithmetic over scalar arguments. A leaf
+  reads one call binding; an inner term applies a Python/NumPy function to
+  its operands. Evaluation walks the tree for each call.
+- Expression, a graph node that stands in for an array. TraceBackend
+  answers the backend protocol by recording nodes; ``fuse`` allows only the
+  elementwise part of the protocol.
 """
 
 import operator
@@ -18,7 +26,7 @@ from types import SimpleNamespace
 import numpy as np
 from numpy.lib.mixins import NDArrayOperatorsMixin
 
-from ._array import ndarray
+from ._array import _reduced_shape, ndarray
 from ._ops import HostScalar, resolve_elementwise
 from .exceptions import BackendMismatchError
 
@@ -30,17 +38,49 @@ class InputRef:
     index: int
 
 
+# ---- host scalar terms ---------------------------------------------------------
+
+
 class ScalarExpression(NDArrayOperatorsMixin):
-    """Host scalar arithmetic captured symbolically and re-evaluated per call."""
+    """Host scalar arithmetic captured symbolically and re-evaluated per call.
+
+    ``sample`` is the value at capture time (it fixes the dtype and NumPy's
+    weak-scalar promotion); ``evaluate(bindings)`` recomputes the value for
+    the bindings of a later call.
+    """
 
     __array_priority__ = 1500
     shape = ()
 
-    def __init__(self, evaluate, sample):
-        self.evaluate = evaluate
+    def __init__(self, function, operands, sample, position=None):
+        self._function = function  # None for a leaf
+        self._operands = tuple(operands)
+        self._position = position  # leaf: index into the bindings
         self.sample = sample
         self.weak_type = type(sample) if type(sample) in (int, float, complex) else None
         self.dtype = np.asarray(sample).dtype
+
+    @classmethod
+    def argument(cls, position, sample):
+        """The scalar bound at ``position`` of each call."""
+        return cls(None, (), sample, position)
+
+    def evaluate(self, bindings):
+        if self._function is None:
+            return bindings[self._position]
+        values = [v.evaluate(bindings) if isinstance(v, ScalarExpression) else v for v in self._operands]
+        with np.errstate(all="ignore"):
+            return self._function(*values)
+
+    @classmethod
+    def apply(cls, function, operands):
+        """A term applying ``function``; NotImplemented next to an array."""
+        if any(isinstance(v, ndarray) for v in operands):
+            return NotImplemented
+        samples = [v.sample if isinstance(v, ScalarExpression) else v for v in operands]
+        with np.errstate(all="ignore"):
+            sample = function(*samples)
+        return cls(function, operands, sample)
 
     def __bool__(self):
         raise TypeError("Data-dependent control flow is not captured; declare static_argnames")
@@ -56,40 +96,43 @@ class ScalarExpression(NDArrayOperatorsMixin):
             raise NotImplementedError("Only plain scalar ufunc calls can be captured")
         if any(isinstance(v, Expression) for v in inputs):
             return trace_op(ufunc, *inputs)
-        return ScalarExpression.combine(ufunc, inputs)
+        return self.apply(ufunc, inputs)
 
-    @staticmethod
-    def combine(function, inputs):
-        if any(isinstance(v, ndarray) for v in inputs):
-            return NotImplemented
+    # Python operators on a captured scalar (NumPy's operators come through
+    # __array_ufunc__; these cover the cases where the other side is a plain
+    # Python number).
+    def __add__(self, other):
+        return self.apply(operator.add, (self, other))
 
-        def resolve(bindings):
-            values = [v.evaluate(bindings) if isinstance(v, ScalarExpression) else v for v in inputs]
-            with np.errstate(all="ignore"):
-                return function(*values)
+    def __radd__(self, other):
+        return self.apply(operator.add, (other, self))
 
-        samples = [v.sample if isinstance(v, ScalarExpression) else v for v in inputs]
-        with np.errstate(all="ignore"):
-            sample = function(*samples)
-        return ScalarExpression(resolve, sample)
+    def __sub__(self, other):
+        return self.apply(operator.sub, (self, other))
+
+    def __rsub__(self, other):
+        return self.apply(operator.sub, (other, self))
+
+    def __mul__(self, other):
+        return self.apply(operator.mul, (self, other))
+
+    def __rmul__(self, other):
+        return self.apply(operator.mul, (other, self))
+
+    def __truediv__(self, other):
+        return self.apply(operator.truediv, (self, other))
+
+    def __rtruediv__(self, other):
+        return self.apply(operator.truediv, (other, self))
+
+    def __neg__(self):
+        return self.apply(operator.neg, (self,))
+
+    def __pos__(self):
+        return self.apply(operator.pos, (self,))
 
 
-def _binary(function, reflected):
-    if reflected:
-        return lambda self, other: ScalarExpression.combine(function, (other, self))
-    return lambda self, other: ScalarExpression.combine(function, (self, other))
-
-
-for _dunder, _function in (
-    ("add", operator.add),
-    ("sub", operator.sub),
-    ("mul", operator.mul),
-    ("truediv", operator.truediv),
-):
-    setattr(ScalarExpression, f"__{_dunder}__", _binary(_function, False))
-    setattr(ScalarExpression, f"__r{_dunder}__", _binary(_function, True))
-ScalarExpression.__neg__ = lambda self: ScalarExpression.combine(operator.neg, (self,))
-ScalarExpression.__pos__ = lambda self: ScalarExpression.combine(operator.pos, (self,))
+# ---- graph nodes ---------------------------------------------------------------
 
 
 class Expression(ndarray):
@@ -98,10 +141,10 @@ class Expression(ndarray):
     __array_priority__ = 2000
 
     def __init__(self, backend, shape, dtype, *, op="input", inputs=(), value=None, resolved=(), attrs=None):
-        self._shape = tuple(shape)
-        self._dtype = np.dtype(dtype)
-        self._backend = backend
-        self._data = self
+        # Storage of a node is the node itself: protocol code that passes
+        # ``array._data`` around keeps working on the graph.
+        self._data, self._backend = self, backend
+        self._shape, self._dtype = tuple(shape), np.dtype(dtype)
         self.op = op
         self.inputs = tuple(inputs)
         self.value = value
@@ -118,9 +161,9 @@ class Expression(ndarray):
         raise TypeError("Host conversion is forbidden during capture")
 
     def __array_ufunc__(self, ufunc, method, *inputs, **kwargs):
-        if method != "__call__" or kwargs.get("out") is not None:
+        plain = method == "__call__" and kwargs.pop("out", None) is None
+        if not plain:
             raise NotImplementedError("Only plain ufunc calls can be captured")
-        kwargs.pop("out", None)
         if kwargs:
             raise NotImplementedError("ufunc options are not captured")
         if ufunc is np.matmul:
@@ -130,10 +173,19 @@ class Expression(ndarray):
         return trace_op(ufunc, *inputs)
 
 
-def _reduced(shape, axes, keepdims):
-    if keepdims:
-        return tuple(1 if i in axes else d for i, d in enumerate(shape))
-    return tuple(d for i, d in enumerate(shape) if i not in axes)
+def _compile_only(capability):
+    """Mark a TraceBackend method as unavailable to ``fuse`` captures."""
+
+    def decorate(method):
+        @wraps(method)
+        def checked(self, *args, **kwargs):
+            if self.elementwise_only:
+                raise NotImplementedError(f"fuse supports elementwise expressions only, not {capability}; use compile")
+            return method(self, *args, **kwargs)
+
+        return checked
+
+    return decorate
 
 
 class TraceBackend:
@@ -143,13 +195,11 @@ class TraceBackend:
 
     def __init__(self, target, *, elementwise_only=False):
         self.target = target
-        self.name = target.name
-        self.device = target.device
+        self.name, self.device = target.name, target.device
         self.elementwise_only = elementwise_only
 
-    def _require_general(self, what):
-        if self.elementwise_only:
-            raise NotImplementedError(f"fuse supports elementwise expressions only, not {what}; use compile")
+    def _record(self, op, shape, dtype, inputs=(), **fields):
+        return Expression(self, shape, dtype, op=op, inputs=inputs, **fields)
 
     def validate_dtype(self, dtype):
         return self.target.validate_dtype(dtype)
@@ -157,16 +207,20 @@ class TraceBackend:
     def wrap(self, data, shape, dtype):
         if not isinstance(data, Expression):
             raise TypeError("Invalid captured storage")
-        if data.shape == tuple(shape) and data.dtype == np.dtype(dtype):
-            return data
-        self._require_general("reshape")
-        return Expression(self, shape, dtype, op="reshape", inputs=(data,))
+        if data.shape != tuple(shape) or data.dtype != np.dtype(dtype):
+            return self._reshape(data, shape, dtype)
+        return data
 
+    @_compile_only("reshape")
+    def _reshape(self, data, shape, dtype):
+        return self._record("reshape", shape, dtype, (data,))
+
+    # Host traffic and uninitialised storage have no place in a plan.
     def upload(self, value):
         value = np.asarray(value)
         if value.ndim:
             raise TypeError("Pass host arrays as explicit OpenPacho arguments before capture")
-        return Expression(self, (), value.dtype, op="scalar", value=HostScalar(value, value.dtype))
+        return self._record("scalar", (), value.dtype, value=HostScalar(value, value.dtype))
 
     def download(self, value):
         raise TypeError("Host observations are forbidden during capture; observe the returned array")
@@ -177,65 +231,61 @@ class TraceBackend:
     def empty(self, shape, dtype):
         raise NotImplementedError("Uninitialized arrays are not captured")
 
-    def full(self, shape, value, dtype):
-        self._require_general("full")
-        return Expression(self, shape, dtype, op="full", attrs={"value": value})
-
     def elementwise(self, name, args, shape, dtype):
         if name == "cast":
-            return Expression(self, shape, dtype, op="cast", inputs=tuple(args), resolved=(args[0].dtype, dtype))
+            return self._record("cast", shape, dtype, tuple(args), resolved=(args[0].dtype, dtype))
         return trace_op(getattr(np, name), *args)
 
-    def gather(self, a, shape, offset, strides):
-        self._require_general("gather")
-        attrs = {"offset": offset, "strides": tuple(strides)}
-        return Expression(self, shape, a.dtype, op="gather", inputs=(a,), attrs=attrs)
+    @_compile_only("full")
+    def full(self, shape, value, dtype):
+        return self._record("full", shape, dtype, attrs={"value": value})
 
+    @_compile_only("gather")
+    def gather(self, a, shape, offset, strides):
+        return self._record("gather", shape, a.dtype, (a,), attrs={"offset": offset, "strides": tuple(strides)})
+
+    @_compile_only("reduce")
     def reduce(self, a, axes, keepdims, dtype, *, operation="sum"):
-        self._require_general("reduce")
         attrs = {"axes": tuple(axes), "keepdims": keepdims}
         if operation != "sum":
             attrs["operation"] = operation
-        return Expression(self, _reduced(a.shape, axes, keepdims), dtype, op="reduce", inputs=(a,), attrs=attrs)
+        return self._record("reduce", _reduced_shape(a.shape, axes, keepdims), dtype, (a,), attrs=attrs)
 
+    @_compile_only("matmul")
     def matmul(self, a, b, shape, dtype):
-        self._require_general("matmul")
-        return Expression(self, shape, dtype, op="matmul", inputs=(a, b))
+        return self._record("matmul", shape, dtype, (a, b))
 
+    @_compile_only("matmul")
     def prepare_padded_matmul(self, ashape, bshape, shape, dtype):
-        self._require_general("matmul")
+        return SimpleNamespace(run=lambda a, b: self._record("matmul", shape, dtype, (a, b), attrs={"padding": True}))
 
-        def run(a, b):
-            return Expression(self, shape, dtype, op="matmul", inputs=(a, b), attrs={"padding": True})
-
-        return SimpleNamespace(run=run)
-
+    @_compile_only("norm")
     def norm(self, a, axes, keepdims, dtype):
-        self._require_general("norm")
         attrs = {"axes": tuple(axes), "keepdims": keepdims}
-        return Expression(self, _reduced(a.shape, axes, keepdims), dtype, op="norm", inputs=(a,), attrs=attrs)
+        return self._record("norm", _reduced_shape(a.shape, axes, keepdims), dtype, (a,), attrs=attrs)
+
+
+def _operand_node(value, dtype, backend):
+    """An elementwise operand as a node of ``backend``'s graph."""
+    if isinstance(value, Expression):
+        return value
+    if isinstance(value, ScalarExpression):
+        return backend._record("scalar", (), dtype, value=value)
+    if np.isscalar(value):
+        return backend._record("scalar", (), dtype, value=HostScalar(value, dtype))
+    raise TypeError("Captured operands must be arrays or numeric scalars")
 
 
 def trace_op(ufunc, *inputs):
     """Record one elementwise operation whose operands include a captured node."""
-    backend = next(v for v in inputs if isinstance(v, Expression))._backend
-    for value in inputs:
-        if isinstance(value, ndarray) and value._backend is not backend:
-            raise BackendMismatchError("Captured arrays must be explicit arguments on the same backend")
-    resolved, shape = resolve_elementwise(ufunc, inputs)
-    for dtype in resolved:
+    backend = next(v._backend for v in inputs if isinstance(v, Expression))
+    if any(isinstance(v, ndarray) and v._backend is not backend for v in inputs):
+        raise BackendMismatchError("Captured arrays must be explicit arguments on the same backend")
+    dtypes, shape = resolve_elementwise(ufunc, inputs)
+    for dtype in dtypes:
         backend.validate_dtype(dtype)
-    operands = []
-    for value, dtype in zip(inputs, resolved):
-        if isinstance(value, Expression):
-            operands.append(value)
-        elif isinstance(value, ScalarExpression):
-            operands.append(Expression(backend, (), dtype, op="scalar", value=value))
-        elif np.isscalar(value):
-            operands.append(Expression(backend, (), dtype, op="scalar", value=HostScalar(value, dtype)))
-        else:
-            raise TypeError("Captured operands must be arrays or numeric scalars")
-    return Expression(backend, shape, resolved[-1], op=ufunc.__name__, inputs=operands, resolved=resolved)
+    nodes = [_operand_node(v, d, backend) for v, d in zip(inputs, dtypes)]
+    return backend._record(ufunc.__name__, shape, dtypes[-1], tuple(nodes), resolved=dtypes)
 
 
 def fuse(function):

@@ -147,48 +147,85 @@ def _hip_backend(device):
     return HIPBackend(device)
 
 
-def _is_backend_object(value):
-    return isinstance(value, NumpyBackend) or getattr(value, "name", None) == "hip"
+class _Selection:
+    """One get_backend request. resolve() tries each step in turn; a step
+    returns the backend, raises, or returns None to pass the request on.
+
+    Semantics follow reference backends.py:190-214 for the names this build
+    provides ('numpy', 'hip'); the reference's other runtimes are reported as
+    unavailable rather than unknown.
+    """
+
+    def __init__(self, target, device, blas, clblast_library):
+        self.target, self.device, self.blas, self.clblast = target, device, blas, clblast_library
+
+    def _configured(self):
+        return any(option is not None for option in (self.device, self.blas, self.clblast))
+
+    def resolve(self):
+        for step in (self._owner, self._provider_options, self._default, self._instance, self._named):
+            found = step()
+            if found is not None:
+                return found
+        raise ValueError("backend must be 'numpy', 'hip', or a backend object")
+
+    def _owner(self):
+        """An array's backend, or a capture's trace backend, as they are."""
+        from ._array import ndarray
+
+        if isinstance(self.target, ndarray):
+            owner, refusal = self.target._backend, "An array's backend cannot be reconfigured"
+        elif getattr(self.target, "_is_tracing", False):
+            owner, refusal = self.target, "Captured backend does not accept reconfiguration"
+        else:
+            return None
+        if self._configured():
+            raise ValueError(refusal)
+        return owner
+
+    def _provider_options(self):
+        """BLAS options belong to 'hip' selected by name; a CLBlast library to
+        a runtime this build does not have."""
+        target = self.target
+        if self.clblast is None and (self.blas is None or target == "hip"):
+            return None
+        if isinstance(target, str) and target in _FOREIGN_RUNTIMES:
+            raise _foreign(target)
+        if self.clblast is not None:
+            raise ValueError("clblast_library requires backend='opencl'")
+        raise ValueError("BLAS configuration requires backend='hip'")
+
+    def _default(self):
+        if self.target is not None:
+            return None
+        if self.device is not None:
+            raise ValueError("device requires backend='hip'")
+        return _DEFAULT.get()
+
+    def _instance(self):
+        if not (isinstance(self.target, NumpyBackend) or getattr(self.target, "name", None) == "hip"):
+            return None
+        if self.device is not None:
+            raise ValueError("device cannot accompany an existing backend")
+        return self.target
+
+    def _named(self):
+        if not isinstance(self.target, str):
+            return None
+        if self.target in _FOREIGN_RUNTIMES:
+            raise _foreign(self.target)
+        if self.target == "hip":
+            if self.blas not in (None, "custom"):
+                raise ValueError("The hip backend has one matrix provider, blas='custom'")
+            return _hip_backend(None if self.device is None else str(self.device))
+        if self.target == "numpy" and self.device is None:
+            return _NUMPY
+        return None
 
 
 def get_backend(backend=None, *, device=None, blas=None, clblast_library=None):
     """Resolve a backend selection, or return an array's own backend."""
-    from ._array import ndarray
-
-    reconfigured = device is not None or blas is not None or clblast_library is not None
-    if isinstance(backend, ndarray):
-        if reconfigured:
-            raise ValueError("An array's backend cannot be reconfigured")
-        return backend._backend
-    if getattr(backend, "_is_tracing", False):
-        if reconfigured:
-            raise ValueError("Captured backend does not accept reconfiguration")
-        return backend
-    if clblast_library is not None:
-        if backend in _FOREIGN_RUNTIMES:
-            raise _foreign(backend)
-        raise ValueError("clblast_library requires backend='opencl'")
-    if blas is not None and backend != "hip":
-        if backend in _FOREIGN_RUNTIMES:
-            raise _foreign(backend)
-        raise ValueError("BLAS configuration requires backend='hip'")
-    if backend is None:
-        if device is not None:
-            raise ValueError("device requires backend='hip'")
-        return _DEFAULT.get()
-    if _is_backend_object(backend):
-        if device is not None:
-            raise ValueError("device cannot accompany an existing backend")
-        return backend
-    if backend == "numpy" and device is None:
-        return _NUMPY
-    if backend == "hip":
-        if blas not in (None, "custom"):
-            raise ValueError("The hip backend has one matrix provider, blas='custom'")
-        return _hip_backend(None if device is None else str(device))
-    if backend in _FOREIGN_RUNTIMES:
-        raise _foreign(backend)
-    raise ValueError("backend must be 'numpy', 'hip', or a backend object")
+    return _Selection(backend, device, blas, clblast_library).resolve()
 
 
 def set_backend(backend, *, device=None, blas=None, clblast_library=None):

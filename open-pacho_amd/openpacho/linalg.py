@@ -17,6 +17,7 @@ def _accepted_order(ord, ndim, axis):
     return (ord == "fro" and matrix) or (ord == 2 and vector)
 
 
+@xp._implements(np.linalg.norm)
 def norm(x, ord=None, axis=None, keepdims=False):
     x = xp.asarray(x)
     if isinstance(axis, tuple) and len(axis) not in (1, 2):
@@ -32,5 +33,3 @@ def norm(x, ord=None, axis=None, keepdims=False):
     data = x._backend.norm(x, axes, keepdims, x.dtype)
     return xp.ndarray._wrap(data, shape, x.dtype, x._backend)
 
-
-xp._FUNCTIONS[np.linalg.norm] = norm

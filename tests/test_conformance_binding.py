@@ -1,16 +1,23 @@
 """Compiled-call binding, residency and generator routing, on NumPy and on hip.
 
-Restates the reference's tests/test_compiled_binding.py:19-156 (the positional
-cache hit skips signature binding; keyword, default, positional-only,
-keyword-only and variadic signatures; static values, shape, dtype and backend
-as specialization keys; plans keep no input alive; the execution scope is
-bound once, from the plan's launch count and not from a backend name),
-tests/test_residency.py:9-27 (NumPy dispatch of elementwise, reduction,
-transpose-product and slicing work on a device array downloads nothing) and
-tests/test_random_routing.py:12-19 (a Generator on a backend instance that is
-not in the name registry uses that instance's implementation). The same body
-runs on the NumPy backend (CPU tier) and, where a device array is involved, on
-hip (``gpu``).
+Contracts (reference tests/test_compiled_binding.py:19-156,
+tests/test_residency.py:9-27, tests/test_random_routing.py:12-19):
+1. a cache hit whose arguments are all positional builds its bindings without
+   signature binding;
+2. keyword and default arguments rebind the same plan; positional-only and
+   keyword-only parameters keep Python's own binding errors; variadic
+   parameters are refused;
+3. static values, array shape, dtype and backend instance are the
+   specialization key, nothing else;
+4. a plan keeps no input array alive;
+5. the execution scope is bound once, when the plan is built, from its launch
+   count against the backend's threshold (never from a backend name);
+6. NumPy dispatch of elementwise, reduction, transpose-product and slicing
+   work on a device array downloads nothing;
+7. a Generator on a backend instance that no name selects uses that
+   instance's implementation.
+Contracts 1, 2, 4 and 6 run on the NumPy backend (CPU tier) and on hip
+(``gpu``); 3, 5 and 7 need several NumPy backend instances and run on CPU.
 """
 
 from __future__ import annotations
@@ -29,164 +36,185 @@ from openpacho.backends import NumpyBackend
 
 @pytest.fixture(params=["numpy", pytest.param("hip", marks=pytest.mark.gpu)])
 def backend(request):
-    if request.param == "numpy":
-        return pacho.get_backend("numpy")
-    return request.getfixturevalue("hip")
+    return pacho.get_backend("numpy") if request.param == "numpy" else request.getfixturevalue("hip")
 
 
-def _array(value, backend, dtype=None):
-    return pacho.asarray(value, dtype=dtype, backend=backend)
+@pytest.fixture
+def bind_calls(monkeypatch):
+    """Every signature binding the compiler performs, recorded."""
+    calls = []
+    real = compiler_module._bind
+
+    def counted(*args, **kwargs):
+        calls.append(args[0])
+        return real(*args, **kwargs)
+
+    monkeypatch.setattr(compiler_module, "_bind", counted)
+    return calls
 
 
-def test_full_positional_cache_hit_skips_signature_bind(backend, monkeypatch):
-    def affine(a, scale):
-        return a * scale + 1
-
-    compiled = pacho.compile(affine)
-    value = np.arange(6, dtype=np.float32)
-    array = _array(value, backend)
-    original_bind = compiler_module._bind
-    bind_calls = []
-
-    def track_bind(*args, **kwargs):
-        bind_calls.append((args, kwargs))
-        return original_bind(*args, **kwargs)
-
-    monkeypatch.setattr(compiler_module, "_bind", track_bind)
-    np.testing.assert_allclose(pacho.asnumpy(compiled(array, 2.0)), value * 2 + 1)
-    np.testing.assert_allclose(pacho.asnumpy(compiled(array, 3.0)), value * 3 + 1)
-    # The miss binds while capturing; the positional hit builds its bindings
-    # straight from the arguments.
-    assert len(bind_calls) == 1
-    assert compiled.cache_info() == {"hits": 1, "misses": 1, "size": 1, "max_size": 32}
+def _host(n=6, dtype=np.float32):
+    return np.arange(n, dtype=dtype)
 
 
-def test_kwargs_and_defaults_reuse_plan_and_rebind_scalars(backend):
-    def affine(a, scale=2.0):
-        return a * scale + 1
-
-    compiled = pacho.compile(affine)
-    value = np.arange(5, dtype=np.float32)
-    array = _array(value, backend)
-    np.testing.assert_allclose(pacho.asnumpy(compiled(array, scale=2.0)), value * 2 + 1)
-    np.testing.assert_allclose(pacho.asnumpy(compiled(array, scale=3.0)), value * 3 + 1)
-    np.testing.assert_allclose(pacho.asnumpy(compiled(array)), value * 2 + 1)
-    assert compiled.cache_info() == {"hits": 2, "misses": 1, "size": 1, "max_size": 32}
+# ---- 1. positional hits bind nothing -----------------------------------------------
 
 
-def test_positional_only_keyword_only_and_variadic_signatures(backend):
-    def positional(a, scale=2.0, /):
-        return a * scale + 1
+def test_positional_hits_skip_binding(backend, bind_calls):
+    def scaled(a, factor):
+        return a * factor - 2
 
-    value = np.arange(4, dtype=np.float32)
-    array = _array(value, backend)
-    compiled = pacho.compile(positional)
-    np.testing.assert_allclose(pacho.asnumpy(compiled(array, 3.0)), value * 3 + 1)
-    # Python's own binding error is kept; 3.10's inspect words it "positional only".
+    compiled = pacho.compile(scaled)
+    x = pacho.asarray(_host(), backend=backend)
+    for factor in (1.5, 2.5, 3.5):
+        np.testing.assert_allclose(pacho.asnumpy(compiled(x, factor)), _host() * factor - 2)
+    assert len(bind_calls) == 1  # the capture of the first call only
+    np.testing.assert_allclose(pacho.asnumpy(compiled(x, factor=4.0)), _host() * 4 - 2)
+    assert len(bind_calls) == 2  # a keyword call binds, and hits the same plan
+    assert compiled.cache_info() == {"hits": 3, "misses": 1, "size": 1, "max_size": 32}
+
+
+# ---- 2. signatures -------------------------------------------------------------------
+
+
+def test_keywords_and_defaults_share_one_plan(backend):
+    def shifted(a, shift=1.0):
+        return a + shift
+
+    compiled = pacho.compile(shifted)
+    x = pacho.asarray(_host(4), backend=backend)
+    for call, want in ((lambda: compiled(x), 1.0), (lambda: compiled(x, shift=5.0), 5.0), (lambda: compiled(x, 7.0), 7.0)):
+        np.testing.assert_allclose(pacho.asnumpy(call()), _host(4) + want)
+    info = compiled.cache_info()
+    assert info["misses"] == 1 and info["hits"] == 2
+
+
+def test_python_binding_rules_are_kept(backend):
+    x = pacho.asarray(_host(3), backend=backend)
+
+    def positional_only(a, k=2.0, /):
+        return a * k
+
+    def keyword_only(a, *, k=2.0):
+        return a * k
+
+    compiled = pacho.compile(positional_only)
+    np.testing.assert_allclose(pacho.asnumpy(compiled(x, 4.0)), _host(3) * 4)
     with pytest.raises(TypeError, match="positional[- ]only"):
-        compiled(array, scale=3.0)
-
-    def keyword_only(a, *, scale=2.0):
-        return a * scale + 1
-
+        compiled(x, k=4.0)
     compiled = pacho.compile(keyword_only)
-    np.testing.assert_allclose(pacho.asnumpy(compiled(array, scale=3.0)), value * 3 + 1)
-    np.testing.assert_allclose(pacho.asnumpy(compiled(array)), value * 2 + 1)
+    np.testing.assert_allclose(pacho.asnumpy(compiled(x, k=4.0)), _host(3) * 4)
+    np.testing.assert_allclose(pacho.asnumpy(compiled(x)), _host(3) * 2)
     with pytest.raises(TypeError):
-        compiled(array, 3.0)
+        compiled(x, 4.0)
 
-    def variadic(a, *rest):
-        return a
 
+@pytest.mark.parametrize("variadic", [lambda a, *more: a, lambda a, **options: a])
+def test_variadic_parameters_are_refused(backend, variadic):
     with pytest.raises(TypeError, match="without \\*args or \\*\\*kwargs"):
-        pacho.compile(variadic)(array)
+        pacho.compile(variadic)(pacho.asarray(_host(2), backend=backend))
 
 
-def test_static_values_and_shape_dtype_backend_remain_specialization_keys():
-    def reshape_to(a, shape):
-        return np.reshape(a, shape)
-
-    compiled = pacho.compile(reshape_to, static_argnames="shape")
-    value = np.arange(6, dtype=np.float32)
-    backend_a, backend_b = NumpyBackend(), NumpyBackend()
-    first = _array(value, backend_a)
-    same = _array(value.copy(), backend_a)
-    different_dtype = _array(value, backend_a, dtype=np.float64)
-    different_backend = _array(value, backend_b)
-    np.testing.assert_array_equal(pacho.asnumpy(compiled(first, (2, 3))), value.reshape(2, 3))
-    np.testing.assert_array_equal(pacho.asnumpy(compiled(same, (2, 3))), value.reshape(2, 3))
-    np.testing.assert_array_equal(pacho.asnumpy(compiled(first, (3, 2))), value.reshape(3, 2))
-    np.testing.assert_array_equal(
-        pacho.asnumpy(compiled(different_dtype, (2, 3))), value.astype(np.float64).reshape(2, 3)
-    )
-    np.testing.assert_array_equal(pacho.asnumpy(compiled(different_backend, (2, 3))), value.reshape(2, 3))
-    assert compiled.cache_info() == {"hits": 1, "misses": 4, "size": 4, "max_size": 32}
+# ---- 3. the specialization key --------------------------------------------------------
 
 
-def test_compiled_plan_does_not_retain_input_arrays(backend):
-    compiled = pacho.compile(lambda a: a * 2 + 1)
-    source = _array(np.arange(7, dtype=np.float32), backend)
-    source_ref = weakref.ref(source)
-    result = compiled(source)
-    del source
+def test_specialization_key_is_static_values_shape_dtype_and_backend():
+    compiled = pacho.compile(lambda a, shape: np.reshape(a, shape), static_argnames="shape")
+    home, other = NumpyBackend(), NumpyBackend()
+    base = _host(12)
+    calls = [
+        (base, np.float32, home, (3, 4), "miss"),
+        (base + 1, np.float32, home, (3, 4), "hit"),  # new values, same key
+        (base, np.float32, home, (4, 3), "miss"),  # static value
+        (base, np.float64, home, (3, 4), "miss"),  # dtype
+        (base, np.float32, other, (3, 4), "miss"),  # backend instance
+        (np.arange(24, dtype=np.float32), np.float32, home, (6, 4), "miss"),  # shape
+        (base * 2, np.float32, other, (3, 4), "hit"),
+    ]
+    misses = hits = 0
+    for values, dtype, owner, shape, outcome in calls:
+        array = pacho.asarray(values, dtype=dtype, backend=owner)
+        np.testing.assert_array_equal(pacho.asnumpy(compiled(array, shape)), values.astype(dtype).reshape(shape))
+        misses += outcome == "miss"
+        hits += outcome == "hit"
+        info = compiled.cache_info()
+        assert (info["misses"], info["hits"]) == (misses, hits)
+
+
+# ---- 4. no retained inputs --------------------------------------------------------------
+
+
+def test_plans_hold_no_reference_to_their_inputs(backend):
+    compiled = pacho.compile(lambda a, b: a * b + a)
+    left = pacho.asarray(_host(9), backend=backend)
+    right = pacho.asarray(_host(9) - 4, backend=backend)
+    watched = [weakref.ref(left), weakref.ref(right)]
+    out = compiled(left, right)
+    del left, right
     gc.collect()
-    assert source_ref() is None
-    np.testing.assert_allclose(pacho.asnumpy(result), np.arange(7, dtype=np.float32) * 2 + 1)
+    assert all(ref() is None for ref in watched)
+    np.testing.assert_allclose(pacho.asnumpy(out), _host(9) * (_host(9) - 4) + _host(9))
 
 
-def test_execution_scope_threshold_is_bound_once_without_backend_name_checks():
+# ---- 5. the execution scope --------------------------------------------------------------
+
+
+def test_execution_scope_is_chosen_when_the_plan_is_built():
     backend = NumpyBackend()
-    events = []
+    log = []
 
     @contextmanager
     def scope():
-        events.append("enter")
-        try:
-            yield
-        finally:
-            events.append("exit")
+        log.append("in")
+        yield
+        log.append("out")
 
     backend.execution_scope = scope
     backend.execution_scope_min_steps = 2
-    a = _array(np.arange(7, dtype=np.float32), backend)
-    for fn in (lambda a: a, lambda a: a + 1):
-        compiled = pacho.compile(fn)
-        compiled(a)
-        assert next(iter(compiled._plans.values()))._execution_scope is None
-    assert events == []
-    compiled = pacho.compile(lambda a: (a + 1) * 2)
-    np.testing.assert_array_equal(pacho.asnumpy(compiled(a)), (np.arange(7) + 1) * 2)
-    # The threshold is read when the plan is built: raising it afterwards
-    # does not unbind the scope of an existing plan.
-    backend.execution_scope_min_steps = 99
-    compiled(a)
-    assert events == ["enter", "exit"] * 2
-    assert compiled.cache_info()["hits"] == 1
+    x = pacho.asarray(_host(5), backend=backend)
+    short = pacho.compile(lambda a: a * 3)  # one launch: below the threshold
+    short(x)
+    assert next(iter(short._plans.values()))._execution_scope is None and log == []
+    long = pacho.compile(lambda a: (a - 1) * 3)  # two launches on a backend without a lowerer
+    np.testing.assert_array_equal(pacho.asnumpy(long(x)), (_host(5) - 1) * 3)
+    assert log == ["in", "out"]
+    backend.execution_scope_min_steps = 50  # read once: an existing plan keeps its scope
+    long(x)
+    assert log == ["in", "out"] * 2
 
 
-def test_numpy_dispatch_does_not_download_arrays(backend, monkeypatch):
-    host = np.arange(12, dtype=np.float32).reshape(3, 4)
+# ---- 6. residency ---------------------------------------------------------------------------
+
+
+def test_numpy_protocol_calls_stay_on_the_device(backend, monkeypatch):
+    host = np.linspace(-2, 2, 20, dtype=np.float32).reshape(4, 5)
     a = pacho.asarray(host, backend=backend)
 
-    def unexpected_download(*args, **kwargs):
-        raise AssertionError("Array operation attempted a host download")
+    def no_download(*args, **kwargs):
+        raise AssertionError("host download")
 
-    with monkeypatch.context() as patch:
-        patch.setattr(backend, "download", unexpected_download)
-        distances = np.sqrt(np.sum((a - 1) ** 2, axis=1))
-        product = np.transpose(a) @ a
-        sliced = a[::-1, ::2]
-        assert distances.backend == product.backend == sliced.backend == backend.name
-    np.testing.assert_allclose(pacho.asnumpy(distances), np.sqrt(np.sum((host - 1) ** 2, axis=1)), rtol=2e-6)
-    np.testing.assert_allclose(pacho.asnumpy(product), host.T @ host)
-    np.testing.assert_array_equal(pacho.asnumpy(sliced), host[::-1, ::2])
+    monkeypatch.setattr(backend, "download", no_download)
+    results = {
+        "elementwise and reduction": np.sqrt(np.sum((a + 1) ** 2, axis=0)),
+        "transpose product": np.transpose(a) @ a,
+        "slice": a[1:, ::-2],
+    }
+    monkeypatch.undo()
+    assert {r.backend for r in results.values()} == {backend.name}
+    np.testing.assert_allclose(pacho.asnumpy(results["elementwise and reduction"]), np.sqrt(np.sum((host + 1) ** 2, axis=0)), rtol=2e-6)
+    np.testing.assert_allclose(pacho.asnumpy(results["transpose product"]), host.T @ host, rtol=2e-6, atol=1e-6)
+    np.testing.assert_array_equal(pacho.asnumpy(results["slice"]), host[1:, ::-2])
 
 
-def test_public_generator_uses_backend_implementation_without_name_registry():
-    class ExampleBackend(NumpyBackend):
-        name = "independent-device"
+# ---- 7. generator routing ---------------------------------------------------------------------
 
-    actual = pacho.random.default_rng(47, backend=ExampleBackend()).normal(size=(3, 5))
-    expected = pacho.random.default_rng(47, backend="numpy").normal(size=(3, 5))
-    assert pacho.get_backend(actual).name == "independent-device"
-    np.testing.assert_array_equal(pacho.asnumpy(actual), pacho.asnumpy(expected))
+
+def test_generator_uses_an_unregistered_backend_instance():
+    class SideBackend(NumpyBackend):
+        name = "side-device"
+
+    side = SideBackend()
+    drawn = pacho.random.default_rng(1234, backend=side).exponential(2.0, size=(4, 3))
+    assert pacho.get_backend(drawn) is side
+    reference = pacho.random.default_rng(1234, backend="numpy").exponential(2.0, size=(4, 3))
+    np.testing.assert_array_equal(pacho.asnumpy(drawn), pacho.asnumpy(reference))

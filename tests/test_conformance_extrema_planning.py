@@ -1,16 +1,17 @@
 """Planning of reductions over materialized inputs (``can_reduce_materialized``).
 
-Restates the reference's tests/test_materialized_extrema.py:83-216 without a
-GPU: a lowering implemented on NumPy stands in for the device, and the hip
-lowering's own capability (float32 min/max) is the native policy.
-- The hook is optional and read from the lowering, never from a backend name.
-- The native capability routes a bare float32 min/max over an array to one
-  map_reduce step with no mapped group; other dtypes and sums stay plain
-  reductions; an elementwise producer still fuses into the map_reduce.
-- A producer shared by two reductions and an elementwise output is computed
-  once per call, rebinds with prepared plans, and nothing is retained.
-- A gather input keeps its own step ahead of the map_reduce.
-- The hip source generator accepts a materialized leaf without a group.
+Contracts (reference tests/test_materialized_extrema.py:83-216), checked
+without a GPU: a lowering that evaluates its groups with NumPy stands in for
+the device, and the hip lowering's own capability (float32 min/max) is the
+native policy.
+1. The hook is optional and read from the lowering, never from a backend name.
+2. With the hip policy, a bare float32 min/max over an array is one map_reduce
+   step with no mapped group; other dtypes and sums stay plain reductions; an
+   elementwise producer still fuses into a map_reduce.
+3. A producer shared by two reductions and an elementwise output is computed
+   once per call, rebinds through prepared plans, and nothing is retained.
+4. A gather input keeps its own step ahead of the map_reduce.
+5. The hip source generator accepts a materialized leaf without a group.
 """
 
 import gc
@@ -27,15 +28,21 @@ from openpacho._hip_lowering import HIPLowering
 from openpacho.backends import NumpyBackend
 
 
-class NumpyLowering:
-    """A lowering that runs every fused and map-reduce group on NumPy and
-    records what the compiler asks of it."""
+def _hip_policy(node):
+    return HIPLowering.can_reduce_materialized(None, node)
 
-    def __init__(self, backend):
+
+class HostLowering:
+    """A lowering whose groups run as NumPy ufuncs on the backend's host
+    storage. It logs each map_reduce request and every array it creates."""
+
+    def __init__(self, backend, policy):
         self.backend = backend
-        self.requests = []  # (node, group, leaves) of each prepare_map_reduce
-        self.outputs = []  # weak references to every mapped array it made
-        self.reduced_inputs = []  # id of the array each reduction read
+        if policy is not None:
+            self.can_reduce_materialized = policy  # an optional hook
+        self.map_reduce_requests = []  # (node, group, leaves)
+        self.created = []  # weak references to mapped results
+        self.reduced_storage = []  # id of the storage each reduction read
 
     def can_residual_matvec(self, *args):
         return False
@@ -44,167 +51,173 @@ class NumpyLowering:
         return tuple(leaves), tuple(group)
 
     def prepare_map_reduce(self, node, group, leaves):
-        self.requests.append((node, tuple(group), tuple(leaves)))
+        self.map_reduce_requests.append((node, tuple(group), tuple(leaves)))
         return tuple(leaves), tuple(group)
 
-    def _evaluate(self, target, group, arguments, operands):
-        known = {id(a): o for a, o in zip(arguments, operands)}
-        for expression in group:
-            inputs = []
-            for child, dtype in zip(expression.inputs, expression.resolved):
-                value = known[id(child)]
-                data = np.asarray(value._data, dtype=dtype).reshape(-1)
-                inputs.append(ndarray._wrap(data, value.shape, dtype, self.backend))
-            data = self.backend.elementwise(expression.op, inputs, expression.shape, expression.dtype)
-            self.outputs.append(weakref.ref(data))
-            known[id(expression)] = ndarray._wrap(data, expression.shape, expression.dtype, self.backend)
-        return known[id(target)]
+    def _value(self, root, group, arguments, operands):
+        """Host array of ``root`` after evaluating the group in order."""
+        table = {id(a): np.asarray(o._data).reshape(o.shape) for a, o in zip(arguments, operands)}
+        for node in group:
+            values = [table[id(c)].astype(d, copy=False) for c, d in zip(node.inputs, node.resolved)]
+            with np.errstate(all="ignore"):
+                table[id(node)] = np.asarray(getattr(np, node.op)(*values), dtype=node.dtype)
+        result = np.ascontiguousarray(np.broadcast_to(table[id(root)], root.shape)).reshape(-1)
+        if group:
+            self.created.append(weakref.ref(result))
+        return result
 
     def run_fused(self, node, payload, arguments, operands):
-        return self._evaluate(node, payload, arguments, operands)._data
+        return self._value(node, payload, arguments, operands)
 
     def run_map_reduce(self, node, payload, arguments, operands):
-        mapped = self._evaluate(node.inputs[0], payload, arguments, operands)
-        self.reduced_inputs.append(id(mapped._data))
-        return self.backend.reduce(
-            mapped, node.attrs["axes"], node.attrs["keepdims"], node.dtype, operation=node.attrs.get("operation", "sum")
-        )
+        source = node.inputs[0]
+        data = self._value(source, payload, arguments, operands)
+        self.reduced_storage.append(id(data) if payload else id(operands[0]._data))
+        mapped = ndarray._wrap(data, source.shape, source.dtype, self.backend)
+        operation = node.attrs.get("operation", "sum")
+        return self.backend.reduce(mapped, node.attrs["axes"], node.attrs["keepdims"], node.dtype, operation=operation)
 
 
-def numpy_device(policy=None, *, name="external"):
-    """A NumPy backend whose lowering optionally offers ``policy`` as its
-    ``can_reduce_materialized`` hook."""
-    attributes = {} if policy is None else {"can_reduce_materialized": policy}
-    lowering = type("Lowering", (NumpyLowering,), attributes)
-
+def _device(policy, name="external"):
     class Device(NumpyBackend):
         def create_lowering(self):
-            return lowering(self)
+            return HostLowering(self, policy)
 
-    backend = Device()
-    backend.name = name
-    return backend
-
-
-def _kinds(compiled, *args):
-    return [step["kind"] for step in compiled.explain(*args)["steps"]]
+    device = Device()
+    device.name = name
+    return device
 
 
-@pytest.mark.parametrize("name", ("hip", "opencl", "cuda", "external"))
-@pytest.mark.parametrize("opt_in", (False, True))
-def test_capability_is_optional_and_independent_of_the_backend_name(name, opt_in):
-    backend = numpy_device((lambda self, node: True) if opt_in else None, name=name)
-    host = np.arange(15, dtype=np.float64).reshape(3, 5)
-    array = p.asarray(host, backend=backend)
-    calculate = p.compile(lambda x: p.max(x, axis=1))
-    np.testing.assert_array_equal(p.asnumpy(calculate(array)), host.max(axis=1))
-    assert _kinds(calculate, array) == ["map_reduce" if opt_in else "reduce"]
+def _plan(compiled):
+    (plan,) = compiled._plans.values()
+    return plan
 
 
-@pytest.mark.parametrize(
-    "dtype,operation,kind",
-    [
-        (np.float32, "min", "map_reduce"),
-        (np.float32, "max", "map_reduce"),
-        (np.float64, "min", "reduce"),
-        (np.float64, "max", "reduce"),
-        (np.int32, "max", "reduce"),
-        (np.bool_, "min", "reduce"),
-        (np.float32, "sum", "reduce"),
-    ],
-)
-def test_hip_capability_limits_the_bare_route_and_keeps_fusion(dtype, operation, kind):
-    backend = numpy_device(HIPLowering.can_reduce_materialized)
-    host = np.arange(15).reshape(3, 5).astype(dtype)
-    array = p.asarray(host, backend=backend)
-    function = getattr(p, operation)
-    bare = p.compile(lambda x: function(x, axis=1))
-    mapped = p.compile(lambda x: function(p.where(x == 0, x, x), axis=1))
-    expected = getattr(np, operation)(host, axis=1, **({"dtype": dtype} if operation == "sum" else {}))
-    for calculate, expected_kind in ((bare, kind), (mapped, "map_reduce")):
-        np.testing.assert_array_equal(p.asnumpy(calculate(array)), expected)
-        assert _kinds(calculate, array) == [expected_kind]
-    if kind == "map_reduce":
-        node, group, leaves = next(iter(bare._plans.values())).lowering.requests[0]
+def _kinds(plan):
+    return [step.kind for step in plan.steps]
+
+
+# ---- 1 -----------------------------------------------------------------------------
+
+
+@pytest.mark.parametrize("hook", [None, lambda node: True])
+@pytest.mark.parametrize("name", ["hip", "cuda", "opencl", "somewhere"])
+def test_the_hook_alone_decides_not_the_backend_name(name, hook):
+    device = _device(hook, name)
+    host = np.linspace(-3, 3, 24).reshape(4, 6)
+    largest = p.compile(lambda x: p.max(x, axis=0))
+    np.testing.assert_array_equal(p.asnumpy(largest(p.asarray(host, backend=device))), host.max(axis=0))
+    assert _kinds(_plan(largest)) == (["reduce"] if hook is None else ["map_reduce"])
+
+
+# ---- 2 -----------------------------------------------------------------------------
+
+NATIVE = [
+    (np.float32, "min", True),
+    (np.float32, "max", True),
+    (np.float64, "max", False),
+    (np.float64, "min", False),
+    (np.int64, "min", False),
+    (np.bool_, "max", False),
+    (np.float32, "sum", False),
+]
+
+
+@pytest.mark.parametrize("dtype,operation,native", NATIVE)
+def test_hip_policy_routes_bare_float32_extrema_only(dtype, operation, native):
+    device = _device(_hip_policy)
+    host = (np.arange(24).reshape(4, 6) % 7).astype(dtype)
+    reduce = getattr(p, operation)
+    bare = p.compile(lambda x: reduce(x, axis=0))
+    produced = p.compile(lambda x: reduce(p.where(x > 2, x, x), axis=0))
+    want = getattr(np, operation)(host, axis=0, **({"dtype": dtype} if operation == "sum" else {}))
+    x = p.asarray(host, backend=device)
+    for compiled in (bare, produced):
+        np.testing.assert_array_equal(p.asnumpy(compiled(x)), want)
+    assert _kinds(_plan(bare)) == (["map_reduce"] if native else ["reduce"])
+    assert _kinds(_plan(produced)) == ["map_reduce"]
+    node, group, leaves = _plan(produced).lowering.map_reduce_requests[0]
+    assert group and node.inputs[0] is group[-1]
+    if native:
+        node, group, leaves = _plan(bare).lowering.map_reduce_requests[0]
         assert group == () and leaves == node.inputs
-    assert next(iter(mapped._plans.values())).lowering.requests[0][1]  # a non-empty mapped group
 
 
-@pytest.mark.parametrize("returned", (False, True))
-def test_shared_producer_is_computed_once_rebound_and_not_retained(returned):
-    backend = numpy_device(HIPLowering.can_reduce_materialized)
-    events, traces = [], []
+# ---- 3 -----------------------------------------------------------------------------
+
+
+@pytest.mark.parametrize("return_producer", [False, True])
+def test_a_shared_producer_runs_once_per_call_and_is_released(return_producer):
+    device = _device(_hip_policy)
+    scopes, captures = [], []
 
     @contextmanager
     def scope():
-        events.append("enter")
-        try:
-            yield
-        finally:
-            events.append("exit")
+        scopes.append("enter")
+        yield
+        scopes.append("exit")
 
-    backend.execution_scope = scope
-    backend.execution_scope_min_steps = 4
+    device.execution_scope = scope
+    device.execution_scope_min_steps = 4
 
     @p.compile
-    def calculate(x, rate):
-        traces.append("trace")
-        shared = x + rate
-        results = (p.min(shared, axis=0), p.max(shared, axis=1), shared * 2)
-        return (shared, *results) if returned else results
+    def statistics(x, offset):
+        captures.append(1)
+        shifted = x + offset
+        outputs = (p.min(shifted, axis=1), p.max(shifted, axis=0), shifted * 3)
+        return (shifted, *outputs) if return_producer else outputs
 
-    host = np.arange(15, dtype=np.float32).reshape(3, 5)
-    first_input = p.asarray(host, backend=backend)
-    first_ref = weakref.ref(first_input)
-    prepared = calculate.prepare(first_input, 2.0)
+    host = np.arange(20, dtype=np.float32).reshape(4, 5)
+    first_input = p.asarray(host, backend=device)
+    first_input_ref = weakref.ref(first_input)
+    prepared = statistics.prepare(first_input, 1.0)
     plan = prepared._plan
-    assert [step[1] for step in plan.steps] == ["fused", "map_reduce", "map_reduce", "fused"]
-    for node, group, leaves in plan.lowering.requests:
-        assert not group and leaves == node.inputs
-        assert leaves[0] is plan.steps[0][0]  # both reductions read the materialized sum
-    backend.execution_scope = lambda: pytest.fail("the plan keeps the scope it was built with")
+    assert _kinds(plan) == ["fused", "map_reduce", "map_reduce", "fused"]
+    producer = plan.steps[0].node
+    for node, group, leaves in plan.lowering.map_reduce_requests:
+        assert group == () and leaves == (producer,)  # both read the materialized sum
+    device.execution_scope = lambda: pytest.fail("a built plan keeps its scope")
 
-    first = calculate(first_input, 2.0)
-    replacement = p.asarray(host * -3, backend=backend)
-    second = prepared(x=replacement, rate=4.0)
-    for actual, shared in ((first, host + 2), (second, host * -3 + 4)):
-        expected = (shared.min(axis=0), shared.max(axis=1), shared * 2)
-        if returned:
-            expected = (shared, *expected)
-        for result, want in zip(actual, expected):
-            np.testing.assert_array_equal(p.asnumpy(result), want)
-    assert traces == ["trace"] and calculate.cache_info()["misses"] == 1
-    assert events == ["enter", "exit"] * 2
-    read = plan.lowering.reduced_inputs
-    assert len(read) == 4 and read[0] == read[1] and read[2] == read[3]
-    assert len(plan.lowering.outputs) == 4  # one add and one multiply per call
-    del first_input, replacement, first, second, actual, result
+    results = [statistics(first_input, 1.0), prepared(x=p.asarray(host - 10, backend=device), offset=-2.0)]
+    for result, shifted in zip(results, (host + 1, host - 12)):
+        want = (shifted.min(axis=1), shifted.max(axis=0), shifted * 3)
+        for got, expected in zip(result, ((shifted, *want) if return_producer else want)):
+            np.testing.assert_array_equal(p.asnumpy(got), expected)
+    assert len(captures) == 1 and statistics.cache_info()["misses"] == 1
+    assert scopes == ["enter", "exit"] * 2
+    read = plan.lowering.reduced_storage
+    assert len(read) == 4 and read[0] == read[1] and read[2] == read[3]  # one producer per call
+    assert len(plan.lowering.created) == 4  # the producer and the product, twice
+    del first_input, results, result, got
     gc.collect()
-    assert first_ref() is None
-    assert all(output() is None for output in plan.lowering.outputs)
+    assert first_input_ref() is None
+    assert not any(ref() is not None for ref in plan.lowering.created)
 
 
-def test_gather_input_keeps_its_own_step():
-    backend = numpy_device(HIPLowering.can_reduce_materialized)
-    host = np.arange(15, dtype=np.float32).reshape(3, 5)
-    array = p.asarray(host, backend=backend)
-    calculate = p.compile(lambda x: p.max(x.T, axis=1, keepdims=True))
-    np.testing.assert_array_equal(p.asnumpy(calculate(array)), host.T.max(axis=1, keepdims=True))
-    plan = next(iter(calculate._plans.values()))
-    assert [step[1] for step in plan.steps] == ["gather", "map_reduce"]
-    node, group, leaves = plan.lowering.requests[0]
-    assert group == () and leaves == node.inputs and leaves[0] is plan.steps[0][0]
+# ---- 4 -----------------------------------------------------------------------------
 
 
-def test_hip_source_accepts_a_materialized_leaf_without_a_mapped_group():
-    backend = numpy_device(HIPLowering.can_reduce_materialized)
-    array = p.asarray(np.zeros((3, 8193), dtype=np.float32), backend=backend)
-    prepared = p.compile(lambda x: p.max(x, axis=1)).prepare(array)
+def test_a_gather_is_its_own_step_before_the_reduction():
+    device = _device(_hip_policy)
+    host = np.arange(20, dtype=np.float32).reshape(4, 5)
+    compiled = p.compile(lambda x: p.min(x.T, axis=1, keepdims=True))
+    np.testing.assert_array_equal(p.asnumpy(compiled(p.asarray(host, backend=device))), host.T.min(axis=1, keepdims=True))
+    plan = _plan(compiled)
+    assert _kinds(plan) == ["gather", "map_reduce"]
+    (node, group, leaves), = plan.lowering.map_reduce_requests
+    assert group == () and leaves == (plan.steps[0].node,)
+
+
+# ---- 5 -----------------------------------------------------------------------------
+
+
+@pytest.mark.parametrize("rows,width,chunks", [(3, 8193, 2), (2, 100, 1), (1, 3 * 8192, 3)])
+def test_hip_source_for_a_materialized_leaf(rows, width, chunks):
+    device = _device(_hip_policy)
+    prepared = p.compile(lambda x: p.max(x, axis=1)).prepare(p.asarray(np.zeros((rows, width), np.float32), backend=device))
     node = prepared._plan.outputs[0]
     lowering = HIPLowering(SimpleNamespace())
     assert lowering.can_reduce_materialized(node)
-    arguments, (source, count, chunks) = lowering.prepare_map_reduce(node, (), node.inputs)
-    assert arguments == node.inputs
-    assert "pacho_map_reduce" in source
-    # 3 rows of 8193 elements: 8192-element chunks, two per row.
-    assert (count, chunks) == (3, 2)
+    arguments, (source, count, per_row) = lowering.prepare_map_reduce(node, (), node.inputs)
+    assert arguments == node.inputs and "pacho_map_reduce" in source
+    assert (count, per_row) == (rows, chunks)  # 8192-element chunks per output row
