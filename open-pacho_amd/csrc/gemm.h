@@ -32,6 +32,20 @@ __device__ __forceinline__ void batch_offsets(int64_t batch, const BatchDesc& bd
   }
 }
 
+// Edge strips of a 2-D fp32 product (gemm_edges.hip): the MFMA kernel takes
+// the whole 256 x 256 tiles and these take strips of at most kEdgeMax rows or
+// columns. a, b, c point at the strip's first element of op(A), op(B) and C;
+// element (r, k) of op(A) is a[r * as_r + k * as_k], element (k, n) of op(B)
+// is b[k * bs_k + n * bs_n]; C rows are ldc long.
+constexpr int kEdgeMax = 8;
+struct Strides {
+  int64_t as_r, as_k, bs_k, bs_n;
+};
+void edge_rows_f32(hp_ctx* ctx, const float* a, const float* b, float* c, int rows, int64_t n, int64_t k,
+                   const Strides& st, int64_t ldc);
+void edge_cols_f32(hp_ctx* ctx, const float* a, const float* b, float* c, int64_t m, int cols, int64_t k,
+                   const Strides& st, int64_t ldc);
+
 // C[b] = op(A[b']) @ op(B[b'']) for b < batch, m x n x k, row-major; op(A)
 // is A stored [k][m] for layout t?, op(B) is B stored [n][k] for ?t.
 using Run = void (*)(hp_ctx* ctx, const void* a, const void* b, void* c, int64_t m, int64_t n, int64_t k,

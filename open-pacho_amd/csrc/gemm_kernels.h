@@ -54,6 +54,11 @@ using hpgemm::BatchDesc;
 
 struct TileMap {
   int64_t tiles_m, tiles_n, tiles_per_batch, total;
+  // Leading dimensions (elements) of A's and B's storage and of C. A product
+  // over a sub-block of larger matrices (the edge split of run_f32) reads and
+  // writes with the full matrices' row lengths; otherwise lda = K or M,
+  // ldb = N or K and ldc = N.
+  int64_t lda, ldb, ldc;
 };
 
 // Division of the tile space between whole-tile workgroups and stream-K
@@ -452,7 +457,7 @@ __global__ __launch_bounds__(kThreads, 1) void kernel(const float* __restrict__ 
   constexpr bool kDirect = decltype(la)::kDirect || decltype(lb)::kDirect;
   la.init(tid);
   lb.init(tid);
-  const int64_t lda = TA ? M : K, ldb = TB ? K : N;
+  const int64_t lda = tmap.lda, ldb = tmap.ldb;
   // Rows read by a lane differ by multiples of 16, so the swizzle of every
   // row it reads equals that of (lane & 15).
   const int a_read = fragment_offset<TA>(wm * WM, lane);
@@ -546,7 +551,7 @@ __global__ __launch_bounds__(kThreads, 1) void kernel(const float* __restrict__ 
     }
 
     if (slot < 0) {
-      float* Cb = C + batch * M * N;
+      float* Cb = C + batch * M * tmap.ldc;
 #pragma unroll
       for (int i = 0; i < FM; ++i) {
 #pragma unroll
@@ -555,7 +560,7 @@ __global__ __launch_bounds__(kThreads, 1) void kernel(const float* __restrict__ 
 #pragma unroll
           for (int r = 0; r < 4; ++r) {
             const int64_t row = ms + Layout::row(wave, i, lane, r);
-            if (MODE == 0 || (row >= m0 && row < M && col >= n0 && col < N)) Cb[row * N + col] = acc[i][j][r];
+            if (MODE == 0 || (row >= m0 && row < M && col >= n0 && col < N)) Cb[row * tmap.ldc + col] = acc[i][j][r];
           }
         }
       }
@@ -698,7 +703,7 @@ __global__ __launch_bounds__(kThreads, 1) void kernel(const double* __restrict__
   constexpr bool kDirect = decltype(la)::kDirect || decltype(lb)::kDirect;
   la.init(tid);
   lb.init(tid);
-  const int64_t lda = TA ? M : K, ldb = TB ? K : N;
+  const int64_t lda = tmap.lda, ldb = tmap.ldb;
   // Fragment rows differ from (lane & 15) by multiples of 16: same swizzle.
   const int sw = swizzle(lane & 15), g = lane >> 4;
   const int a_read0 = (wm * WM + (lane & 15)) * S + 2 * (g ^ sw);
@@ -791,7 +796,7 @@ __global__ __launch_bounds__(kThreads, 1) void kernel(const double* __restrict__
     }
 
     if (slot < 0) {
-      double* Cb = C + batch * M * N;
+      double* Cb = C + batch * M * tmap.ldc;
 #pragma unroll
       for (int i = 0; i < FM; ++i) {
 #pragma unroll
@@ -800,7 +805,7 @@ __global__ __launch_bounds__(kThreads, 1) void kernel(const double* __restrict__
 #pragma unroll
           for (int r = 0; r < 4; ++r) {
             const int64_t row = m0 + Layout::row(wave, i, lane, r);
-            if (MODE == 0 || (row < M && col < N)) Cb[row * N + col] = acc[i][j][r];
+            if (MODE == 0 || (row < M && col < N)) Cb[row * tmap.ldc + col] = acc[i][j][r];
           }
         }
       }
@@ -856,19 +861,23 @@ __global__ __launch_bounds__(256) void fixup_kernel(T* __restrict__ C, int64_t M
   const int j = block % FN;
   int64_t batch, ti, tj;
   logical_tile(sp.dp_tiles + tl, tmap, batch, ti, tj);
-  T* Cb = C + batch * M * N;
+  T* Cb = C + batch * M * tmap.ldc;
   // The tile was computed at its (possibly moved) origin, as in the kernels.
   const int64_t m0 = ti * BM, n0 = tj * BN;
   const int64_t col = (sp.moved ? tile_origin(n0, N, BN) : n0) + L::col(wave, j, lane);
 #pragma unroll
   for (int r = 0; r < 4; ++r) {
     const int64_t row = (sp.moved ? tile_origin(m0, M, BM) : m0) + L::row(wave, i, lane, r);
-    if (row >= m0 && row < M && col >= n0 && col < N) Cb[row * N + col] = sum[r];
+    if (row >= m0 && row < M && col >= n0 && col < N) Cb[row * tmap.ldc + col] = sum[r];
   }
 }
 
 
-void prepare(int64_t m, int64_t n, int64_t batch, int64_t bm, int64_t bn, TileMap& tm) {
+void prepare(int64_t m, int64_t n, int64_t batch, int64_t bm, int64_t bn, TileMap& tm, int64_t lda, int64_t ldb,
+             int64_t ldc) {
+  tm.lda = lda;
+  tm.ldb = ldb;
+  tm.ldc = ldc;
   tm.tiles_m = hp::ceil_div(m, bm);
   tm.tiles_n = hp::ceil_div(n, bn);
   tm.tiles_per_batch = tm.tiles_m * tm.tiles_n;
@@ -944,20 +953,33 @@ int mode_of(int64_t m, int64_t n, int64_t k, int64_t bm, int64_t bn, int64_t bk)
   return m % bm == 0 && n % bn == 0 ? 0 : 1;
 }
 
+// Modes 0 and 1 load the k-contiguous operands (A unless TA, B if TB)
+// straight into LDS with 16-byte LDS-DMA, which needs every row of every
+// batch matrix 16-byte aligned. K % 16 == 0 in those modes, so rows inside a
+// matrix follow from its origin: the base pointer and each batch stride must
+// be multiples of 16 bytes. Mode 2's register-staged loads serve the rest.
+template <typename T, bool TA, bool TB>
+bool dma_aligned(const T* a, const T* b, const BatchDesc& bd) {
+  auto aligned = [&](const T* p, const int64_t* strides) {
+    if (reinterpret_cast<uintptr_t>(p) % 16 != 0) return false;
+    for (int d = 0; d < bd.rank; ++d)
+      if ((strides[d] * int64_t(sizeof(T))) % 16 != 0) return false;
+    return true;
+  };
+  return (TA || aligned(a, bd.a_stride)) && (!TB || aligned(b, bd.b_stride));
+}
+
+// The tiled MFMA product over an m x n block whose B and C rows are ldb and
+// ldc elements long.
 template <bool TA, bool TB>
-void run_f32(hp_ctx* ctx, const float* a, const float* b, float* c, int64_t m, int64_t n, int64_t k,
-             const BatchDesc& bd, int64_t batch) {
+void run_f32_tiles(hp_ctx* ctx, const float* a, const float* b, float* c, int64_t m, int64_t n, int64_t k,
+                   const BatchDesc& bd, int64_t batch, int64_t lda, int64_t ldb, int64_t ldc) {
   using namespace f32;
   TileMap tm;
-  prepare(m, n, batch, BM, BN, tm);
+  prepare(m, n, batch, BM, BN, tm, lda, ldb, ldc);
   auto fix = fixup_kernel<float, hpd::f32x4, Layout>;
   int mode = mode_of(m, n, k, BM, BN, BK);
-  // Modes 0 and 1 load the k-contiguous operands (A unless TA, B if TB)
-  // straight into LDS, which needs 16-byte aligned rows. K % 16 == 0 there,
-  // so the base pointers decide; mode 2's register-staged loads serve views
-  // at other element offsets.
-  const bool aligned = (TA || reinterpret_cast<uintptr_t>(a) % 16 == 0) && (!TB || reinterpret_cast<uintptr_t>(b) % 16 == 0);
-  if (!aligned) mode = 2;
+  if (!dma_aligned<float, TA, TB>(a, b, bd)) mode = 2;
   switch (mode) {
     case 0:
       launch_split<float, BM, BN>(ctx, kernel<0, false, TA, TB>, kernel<0, true, TA, TB>, fix, kThreads, a, b, c, m,
@@ -973,18 +995,45 @@ void run_f32(hp_ctx* ctx, const float* a, const float* b, float* c, int64_t m, i
   }
 }
 
+// A 2-D product (any operand layout) whose last tile row (column) would hold
+// at most kEdgeMax rows (columns) runs as three parts: the MFMA kernel on the
+// whole tiles, the edge columns strip for the other rows, the edge rows strip
+// for every column (gemm_edges.hip). The same split for every layout keeps a
+// product of transposed operands bit-identical to the product of their
+// materialized transposes. Otherwise the whole product is tiled, edge tiles
+// included.
+template <bool TA, bool TB>
+void run_f32(hp_ctx* ctx, const float* a, const float* b, float* c, int64_t m, int64_t n, int64_t k,
+             const BatchDesc& bd, int64_t batch) {
+  using f32::BM;
+  using f32::BN;
+  const int64_t lda = TA ? m : k, ldb = TB ? k : n;
+  if (batch == 1) {
+    const int64_t rows = m % BM, cols = n % BN;
+    const bool split_rows = m > BM && rows > 0 && rows <= hpgemm::kEdgeMax;
+    const bool split_cols = n > BN && cols > 0 && cols <= hpgemm::kEdgeMax;
+    if (split_rows || split_cols) {
+      const int64_t mt = split_rows ? m - rows : m, nt = split_cols ? n - cols : n;
+      // op(A)(r, k) and op(B)(k, n) in the stored layouts.
+      const hpgemm::Strides st{TA ? 1 : k, TA ? m : 1, TB ? 1 : n, TB ? k : 1};
+      run_f32_tiles<TA, TB>(ctx, a, b, c, mt, nt, k, bd, 1, lda, ldb, n);
+      if (split_cols) hpgemm::edge_cols_f32(ctx, a, b + nt * st.bs_n, c + nt, mt, int(cols), k, st, n);
+      if (split_rows) hpgemm::edge_rows_f32(ctx, a + mt * st.as_r, b, c + mt * n, int(rows), n, k, st, n);
+      return;
+    }
+  }
+  run_f32_tiles<TA, TB>(ctx, a, b, c, m, n, k, bd, batch, lda, ldb, n);
+}
+
 template <bool TA, bool TB>
 void run_f64(hp_ctx* ctx, const double* a, const double* b, double* c, int64_t m, int64_t n, int64_t k,
              const BatchDesc& bd, int64_t batch) {
   using namespace f64;
   TileMap tm;
-  prepare(m, n, batch, BM, BN, tm);
+  prepare(m, n, batch, BM, BN, tm, TA ? m : k, TB ? k : n, n);
   auto fix = fixup_kernel<double, f64x4, Layout>;
   int mode = mode_of(m, n, k, BM, BN, BK);
-  // Modes 0 and 1 load k-contiguous operands with LDS-DMA (16-byte aligned
-  // rows, as in run_f32); views at other element offsets use mode 2.
-  const bool aligned = (TA || reinterpret_cast<uintptr_t>(a) % 16 == 0) && (!TB || reinterpret_cast<uintptr_t>(b) % 16 == 0);
-  if (!aligned) mode = 2;
+  if (!dma_aligned<double, TA, TB>(a, b, bd)) mode = 2;
   switch (mode) {
     case 0:
       launch_split<double, BM, BN>(ctx, kernel<0, false, TA, TB>, kernel<0, true, TA, TB>, fix, kThreads, a, b, c,

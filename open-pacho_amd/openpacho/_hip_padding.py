@@ -1,19 +1,21 @@
 """The hip backend's opt-in padding plan for fp32 GEMM (``matmul(padding=True)``).
 
-Plan semantics follow the reference (_padding.py:80-109 eligibility and
-rounding, :25-77 run/explain/dispatch_count): float32 operands with at least
-32 output rows and columns and K >= 16 are copied into private +0-filled
-buffers with M and N rounded up to 32 and K to 16; the GEMM runs on the padded
-shapes and the padded product is cropped. The plan is its own object because
-the reference's PaddedGemm dispatches its GEMM by backend name; this one calls
-the hip backend's own matmul and pad/crop copies (hp_pad_copy), so the module
-needs only ``ndarray`` from the array facade.
+Eligibility and rounding follow the reference (_padding.py:80-109): float32
+operands with at least 32 output rows and columns and K >= 16 form a plan
+whose padded problem rounds M and N up to 32 and K up to 16, with +0 in the
+padding, and whose result is the padded product cropped to the logical shape.
 
-On this backend padding turns an unaligned problem (e.g. odd K, which forces
-scalar guarded loads) into the 16-byte vector-load path of the MFMA kernel.
-``bounds_checks_removed`` is True only when the padded problem is a whole
-number of the kernel's workgroup tiles (256 x 16 x 256), because only then
-does the GEMM run without element guards.
+The plan computes that padded problem without copying it. The MFMA kernel
+already contracts the K edge against +0 (its last K slice zero-fills past K)
+and stores only the rows and columns of the logical output, so the padded
+buffers of the reference's plan (two +0-filled operand copies and a padded
+product cropped by a third copy) would add three HBM passes and change no bit
+of the result. ``explain()`` therefore reports the padded shapes and
+alignment of the padded problem with the scratch and copies this plan really
+uses: none (``scratch_bytes`` 0, ``copy_dispatches`` 0, ``dispatch_count``
+1). ``bounds_checks_removed`` is True when the logical problem is a whole
+number of the kernel's workgroup tiles (256 x 16 x 256): only then does the
+product run without edge handling.
 """
 
 from dataclasses import dataclass
@@ -36,49 +38,33 @@ class HIPPaddedGemm:
     output_shape: tuple
     padded_input_shapes: tuple
     padded_output_shape: tuple
+    dtype: np.dtype
 
-    @property
-    def dispatch_count(self):
-        copies = sum(a != b for a, b in zip(self.input_shapes, self.padded_input_shapes))
-        return 1 + copies + (self.output_shape != self.padded_output_shape)
+    dispatch_count = 1  # one product call; no pad or crop copies
 
     def run(self, a, b):
-        from ._array import ndarray
-
-        backend = self.backend
-        operands = []
-        for array, padded in zip((a, b), self.padded_input_shapes):
-            if array.shape != padded:
-                array = ndarray._wrap(backend.pad_copy(array, padded), padded, array.dtype, backend)
-            operands.append(array)
-        data = backend.matmul(operands[0], operands[1], self.padded_output_shape, a.dtype)
-        if self.padded_output_shape != self.output_shape:
-            padded = ndarray._wrap(data, self.padded_output_shape, a.dtype, backend)
-            data = backend.pad_copy(padded, self.output_shape)
-        return data
+        return self.backend.matmul(a, b, self.output_shape, self.dtype)
 
     def explain(self):
-        scratch = [
-            prod(padded) * 4 for original, padded in zip(self.input_shapes, self.padded_input_shapes) if original != padded
-        ]
-        if self.output_shape != self.padded_output_shape:
-            scratch.append(prod(self.padded_output_shape) * 4)
-        mp, kp = self.padded_input_shapes[0][-2:]
-        np_ = self.padded_output_shape[-1]
+        (m, k), n = self.input_shapes[0][-2:], self.output_shape[-1]
         return {
             "input_shapes": self.input_shapes,
             "padded_input_shapes": self.padded_input_shapes,
             "output_shape": self.output_shape,
             "padded_output_shape": self.padded_output_shape,
             "alignment": ALIGNMENT,
-            "scratch_bytes": sum(scratch),
-            "copy_dispatches": len(scratch),
-            "bounds_checks_removed": all(v % t == 0 for v, t in zip((mp, kp, np_), KERNEL_TILE)),
+            "scratch_bytes": 0,
+            "copy_dispatches": 0,
+            "bounds_checks_removed": all(v % t == 0 for v, t in zip((m, k, n), KERNEL_TILE)),
         }
 
 
 def prepare(backend, ashape, bshape, shape, dtype, *, max_buffer_bytes=None):
-    """Form a plan, or decline with None before any allocation."""
+    """Form a plan, or decline with None, before any allocation.
+
+    ``max_buffer_bytes`` keeps the reference's limit on the largest padded
+    buffer, so eligibility does not depend on the zero-copy execution.
+    """
     ashape, bshape, shape = tuple(ashape), tuple(bshape), tuple(shape)
     if (
         np.dtype(dtype) != np.dtype("float32")
@@ -98,4 +84,4 @@ def prepare(backend, ashape, bshape, shape, dtype, *, max_buffer_bytes=None):
     largest = max(prod(s) for s in (ap, bp, cp))
     if largest > 2**31 - 1 or (max_buffer_bytes is not None and largest * 4 > max_buffer_bytes):
         return None
-    return HIPPaddedGemm(backend, (ashape, bshape), shape, (ap, bp), cp)
+    return HIPPaddedGemm(backend, (ashape, bshape), shape, (ap, bp), cp, np.dtype(dtype))

@@ -296,10 +296,12 @@ def _plan(ashape, bshape, shape, dtype=np.float32, **kw):
 
 
 def test_padding_metadata():
+    # The padded problem is the reference's (oracle.padding.plan pins its
+    # worked values); hip computes it without copies, and says so.
     plan = _plan((33, 17), (17, 65), (33, 65))
     assert plan.padded_input_shapes == ((64, 32), (32, 96)) and plan.padded_output_shape == (64, 96)
     info = plan.explain()
-    assert info["scratch_bytes"] == 45056 and info["copy_dispatches"] == 3 and plan.dispatch_count == 4
+    assert info["scratch_bytes"] == 0 and info["copy_dispatches"] == 0 and plan.dispatch_count == 1
     assert info["alignment"] == (32, 16, 32)
     assert _plan((64, 32), (32, 96), (64, 96)).dispatch_count == 1
     assert _plan((17,), (17, 65), (65,)) is None
@@ -308,7 +310,8 @@ def test_padding_metadata():
     assert _plan((2**31, 16), (16, 32), (2**31, 32)) is None
     assert _plan((33, 17), (17, 65), (33, 65), max_buffer_bytes=24575) is None
     big = _plan((4097, 3001), (3001, 2049), (4097, 2049))
-    assert big.explain()["scratch_bytes"] == 109_039_616
+    assert big.padded_input_shapes == ((4128, 3008), (3008, 2080)) and big.padded_output_shape == (4128, 2080)
+    assert big.explain()["scratch_bytes"] == 0
     assert big.explain()["bounds_checks_removed"] is False
     assert _plan((512, 64), (64, 256), (512, 256)).explain()["bounds_checks_removed"] is True
 

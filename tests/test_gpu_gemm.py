@@ -256,9 +256,11 @@ def test_config4_padded_odd_shape(hip):
     assert len(step) == 1
     info = step[0]["padding"]
     expected = pad_oracle.plan((m, k), (k, n))
+    # The reference's padded problem, computed without its copies.
     assert info["padded_input_shapes"] == expected["padded_input_shapes"]
-    assert info["scratch_bytes"] == expected["scratch_bytes"] == 109_039_616
-    assert info["copy_dispatches"] == 3 and info["alignment"] == (32, 16, 32)
+    assert info["padded_output_shape"] == expected["padded_output_shape"]
+    assert expected["scratch_bytes"] == 109_039_616 and info["scratch_bytes"] == 0
+    assert info["copy_dispatches"] == 0 and info["alignment"] == (32, 16, 32)
     for result in (p.matmul(A, B, padding=True), compiled(A, B)):
         got = p.asnumpy(result)
         assert got.shape == (m, n)
@@ -293,7 +295,7 @@ def test_padding_rounds_to_tiles_and_preserves_logical_results(hip, shapes):
     plan = pad_oracle.plan(*shapes)
     assert tuple(step["padded_input_shapes"]) == plan["padded_input_shapes"]
     assert tuple(step["padded_output_shape"]) == plan["padded_output_shape"]
-    assert step["scratch_bytes"] == plan["scratch_bytes"]
+    assert step["scratch_bytes"] == 0 and step["copy_dispatches"] == 0
     expected = left.astype(np.float64) @ right.astype(np.float64)
     prepared = compiled.prepare(a, b)
     first = compiled(a, b)
@@ -478,3 +480,71 @@ def test_bool_gemm_abi_is_or_of_ands(hip):
     with hip._active():
         hip._call("hp_gemm", 0, *hip._ptrs(A, B, out), 19, 21, 33, 0, None, None, None)
     np.testing.assert_array_equal(p.asnumpy(out), a @ b)
+
+
+@pytest.mark.parametrize("dtype", [np.float32, np.float64])
+def test_batch_strides_off_the_16_byte_grid(hip, dtype):
+    """hp_gemm with an A batch stride of m*k + 1 elements: every other batch
+    matrix starts off a 16-byte boundary, so the product must take the
+    register-staged loads, not LDS-DMA (M, N, K would otherwise allow it)."""
+    from openpacho import _hip_lib
+
+    m, n, k, batch = 256, 256, 32, 3
+    stride = m * k + 1
+    rng = np.random.default_rng(stride)
+    a_host = rng.uniform(-1, 1, stride * batch).astype(dtype)
+    b_host = rng.uniform(-1, 1, (k, n)).astype(dtype)
+    A, B = hip.upload(a_host), hip.upload(b_host)
+    C = hip.upload(np.full(batch * m * n, np.nan, dtype))
+    code = _hip_lib.DTYPE_CODES[np.dtype(dtype)]
+    with hip._active():
+        hip._call("hp_gemm", code, *hip._ptrs(A, B, C), m, n, k, 1, _hip_lib.int64_array([batch]),
+                  _hip_lib.int64_array([stride]), _hip_lib.int64_array([0]))
+    got = p.asnumpy(p.ndarray._wrap(C, (batch, m, n), dtype, hip))
+    bound = (4e-7 if dtype == np.float32 else 8e-16) * np.sqrt(k) * 4
+    for i in range(batch):
+        a_i = a_host[i * stride : i * stride + m * k].reshape(m, k).astype(np.float64)
+        want = a_i @ b_host.astype(np.float64)
+        scale = np.abs(a_i) @ np.abs(b_host.astype(np.float64))
+        assert np.all(np.abs(got[i] - want) <= bound * scale + 1e-30), i
+
+
+# Products whose last tile row or column holds at most 8 rows or columns run
+# as whole 256 x 256 tiles plus edge strips (the few-rows kernel reads B once
+# with K cut into chunks, the few-columns kernel streams A rows).
+EDGE_CASES = [
+    (257, 300, 512),  # one edge row; 44 edge columns stay in tiles
+    (520, 264, 1000),  # 8 rows and 8 columns
+    (263, 1031, 77),  # 7 and 7, odd K: two K chunks of the rows strip
+    (1280, 513, 3001),  # one edge column, odd K
+    (4097, 4097, 16),  # one row and one column, one K slice (rows strip written directly)
+    (300, 2305, 4096),  # one edge column beside 44 rows in tiles
+]
+
+
+@pytest.mark.parametrize("m,k,n", EDGE_CASES)
+def test_edge_strips_against_float64_and_repeatable(hip, m, k, n):
+    rng = np.random.default_rng(m * 5 + k + n)
+    a = rng.uniform(-1, 1, (m, k)).astype(np.float32)
+    b = rng.uniform(-1, 1, (k, n)).astype(np.float32)
+    A, B = p.asarray(a, backend=hip), p.asarray(b, backend=hip)
+    got = p.asnumpy(A @ B)
+    np.testing.assert_array_equal(got, p.asnumpy(A @ B))
+    want = a.astype(np.float64) @ b.astype(np.float64)
+    scale = np.abs(a).astype(np.float64) @ np.abs(b).astype(np.float64)
+    assert np.all(np.abs(got - want) <= 4e-7 * np.sqrt(k) * 4 * scale + 1e-30)
+    edge_rows = m % 256 if m > 256 and m % 256 <= 8 else 0
+    edge_cols = n % 256 if n > 256 and n % 256 <= 8 else 0
+    rows = np.r_[0:4, m - edge_rows - 1 : m]  # the last tile row and the strip
+    cols = np.r_[0:4, n - edge_cols - 1 : n]
+    hip_err, ref_err = _sampled_error_ratio(a, b, got, 64, m + n)
+    assert hip_err <= 2 * ref_err
+    strip = [(r, c) for r in rows for c in cols if r >= m - edge_rows or c >= n - edge_cols]
+    if strip:
+        rr, cc = np.array(strip).T
+        ref = kernels.gemm_sequential(a, b, rr, cc)
+        truth = np.array([float(exact.exact_dot(a[r], b[:, c])) for r, c in strip])
+        mag = np.array([float(exact.exact_dot(np.abs(a[r]), np.abs(b[:, c]))) for r, c in strip])
+        hip_strip = np.sqrt(np.mean(((got[rr, cc] - truth) / mag) ** 2))
+        ref_strip = np.sqrt(np.mean(((ref - truth) / mag) ** 2))
+        assert hip_strip <= 2 * ref_strip + 2.0**-24
