@@ -267,11 +267,29 @@ constexpr unsigned kWaitVmcnt0 = 0x0F70;
 
 namespace f32 {
 
-constexpr int BM = 256, BN = 256, BK = 16;
+constexpr int BK = 16;
 constexpr int S = BK;  // LDS row stride (floats): 16-float rows, swizzled quads
-constexpr int kThreads = 512;
-constexpr int FM = 8, FN = 4;  // MFMA blocks per wave
-constexpr int WM = 128, WN = 64;
+
+// A workgroup tile configuration: BM x BN tile, waves in a WAVES_M x WAVES_N
+// grid of WM x WN wave tiles (FM x FN MFMA blocks of 16 x 16 per wave),
+// MIN_BLOCKS workgroups resident per compute unit.
+template <int BM_, int BN_, int WAVES_M_, int WAVES_N_, int MIN_BLOCKS_>
+struct Tile {
+  static constexpr int BM = BM_, BN = BN_, WAVES_M = WAVES_M_, WAVES_N = WAVES_N_;
+  static constexpr int kThreads = 64 * WAVES_M * WAVES_N;
+  static constexpr int WM = BM / WAVES_M, WN = BN / WAVES_N;
+  static constexpr int FM = WM / 16, FN = WN / 16;
+  static constexpr int kMinBlocks = MIN_BLOCKS_;
+  // The staged slice goes to LDS after the MFMAs of this A fragment.
+  static constexpr int kCommitAfter = FM - 3;
+  static_assert(FM >= 4 && FN <= FM, "B refills ride on the first FN A fragments");
+};
+// 256 x 256, 8 waves of 128 x 64, one workgroup per compute unit: the
+// headline tile (fewest operand loads per flop).
+using Big = Tile<256, 256, 2, 4, 1>;
+// 128 x 128, 4 waves of 64 x 64, two workgroups per compute unit: four times
+// the tiles of Big, for products whose Big tiles do not fill the chip.
+using Small = Tile<128, 128, 2, 2, 2>;
 
 // LDS rows hold 4 quads of 4 consecutive k values; quad q of row r is stored
 // at slot q ^ ((r >> 1) & 3). Rows are 16 floats (64 B), so a ds_read_b128 by
@@ -291,10 +309,10 @@ __device__ __forceinline__ int swizzle(int row) { return (row >> 1) & 3; }
 // 89.0% of peak, 4096^3 83.8% -> 88.1%.
 constexpr int PS = 20;
 
-template <int MODE>
+template <int ROWS, int THREADS, int MODE>
 struct PairLoader {
   static_assert(MODE != 1, "mode 1 moves edge tiles inside the operands and uses the interior loader");
-  static_assert(kThreads == 512 && BM == 256 && BN == 256, "8 k pairs x 64 row blocks of 4 per slice");
+  static_assert(ROWS == THREADS / 2, "8 k pairs x THREADS / 8 row blocks of 4 per slice");
   hpd::f32x4 v[2];
   int kh, b;
 
@@ -310,7 +328,7 @@ struct PairLoader {
   __device__ __forceinline__ void load(const float* p, int64_t r0, int64_t rows, int64_t ld, int64_t kp,
                                        int64_t k0) {
     const int64_t c = r0 + 4 * b;
-    if (MODE == 2 && (k0 + 16 > kp || r0 + BN > rows)) {
+    if (MODE == 2 && (k0 + 16 > kp || r0 + ROWS > rows)) {
 #pragma unroll
       for (int r = 0; r < 2; ++r) {
         const int64_t k = k0 + 2 * kh + r;
@@ -352,21 +370,22 @@ struct PairLoader {
 // swizzle places at its position: row 16c + l / 4, k group (l % 4) ^
 // swizzle(row). Completion is tracked by vmcnt; kernels wait for vmcnt(0)
 // before the barrier that publishes a slice. Every row read is in bounds.
-template <int MODE>
+template <int ROWS, int THREADS, int MODE>
 struct DmaLoader {
   static_assert(MODE == 0, "in-bounds rows only: mode 1 moves edge tiles inside, mode 2 stages");
-  static_assert(kThreads == 512 && BM == 256 && BN == 256, "16 chunks of 16 rows per slice");
+  static constexpr int kChunks = ROWS / 16 / (THREADS / 64);  // 16-row chunks per wave
+  static_assert(kChunks * 16 * (THREADS / 64) == ROWS, "whole 16-row chunks per wave");
   int chunk0, lane;
 
   __device__ __forceinline__ void init(int tid) {
-    chunk0 = 2 * __builtin_amdgcn_readfirstlane(tid >> 6);
+    chunk0 = kChunks * __builtin_amdgcn_readfirstlane(tid >> 6);
     lane = tid & 63;
   }
 
   __device__ __forceinline__ void issue(const float* p, int64_t r0, int64_t rows, int64_t ld, int64_t, int64_t k0,
                                         float* buf) const {
 #pragma unroll
-    for (int i = 0; i < 2; ++i) {
+    for (int i = 0; i < kChunks; ++i) {
       const int c = chunk0 + i;
       const int row = 16 * c + (lane >> 2);
       const float* src = p + (r0 + row) * ld + k0 + 4 * ((lane & 3) ^ swizzle(row));
@@ -382,8 +401,8 @@ struct DmaLoader {
 };
 
 // Register-staged k-contiguous loads (mode 2: the K-edge slice zero-fills).
-template <int MODE>
-struct StagedLoader : SliceLoader<float, 256, false, MODE, kThreads> {
+template <int ROWS, int THREADS, int MODE>
+struct StagedLoader : SliceLoader<float, ROWS, false, MODE, THREADS> {
   __device__ __forceinline__ void issue(const float* p, int64_t r0, int64_t rows, int64_t ld, int64_t kp, int64_t k0,
                                         float*) {
     this->load(p, r0, rows, ld, kp, k0);
@@ -400,10 +419,11 @@ constexpr int lds_stride() {
 }
 // Modes 0 and 1 share the interior loaders: mode 1 (M, N >= one tile) moves
 // edge tiles inside the operands instead of clamping their rows.
-template <bool KM, int MODE>
+template <bool KM, int MODE, int ROWS, int THREADS>
 using Loader = typename std::conditional<
-    KM, PairLoader<MODE == 1 ? 0 : MODE>,
-    typename std::conditional<MODE == 2, StagedLoader<MODE>, DmaLoader<MODE == 1 ? 0 : MODE>>::type>::type;
+    KM, PairLoader<ROWS, THREADS, MODE == 1 ? 0 : MODE>,
+    typename std::conditional<MODE == 2, StagedLoader<ROWS, THREADS, MODE>,
+                              DmaLoader<ROWS, THREADS, MODE == 1 ? 0 : MODE>>::type>::type;
 
 // Fragment read offset of lane `lane` for tile row `row0 + (lane & 15)`.
 template <bool KM>
@@ -412,48 +432,60 @@ __device__ __forceinline__ int fragment_offset(int row0, int lane) {
   return KM ? row * PS + 4 * (lane >> 4) : row * S + 4 * ((lane >> 4) ^ swizzle(lane & 15));
 }
 
-// Eight waves in a 2x4 grid of 128x64 wave tiles. Accumulator layout: lane
+// Waves in a WAVES_M x WAVES_N grid of wave tiles. Accumulator layout: lane
 // holds column lane%16, rows 4*(lane/16) + r.
+template <class T>
 struct Layout {
-  static constexpr int kBM = BM, kBN = BN, kFM = FM, kFN = FN;
+  static constexpr int kBM = T::BM, kBN = T::BN, kFM = T::FM, kFN = T::FN;
   static __device__ __forceinline__ int row(int wave, int i, int lane, int r) {
-    return (wave >> 2) * WM + 16 * i + 4 * (lane >> 4) + r;
+    return (wave / T::WAVES_N) * T::WM + 16 * i + 4 * (lane >> 4) + r;
   }
-  static __device__ __forceinline__ int col(int wave, int j, int lane) { return (wave & 3) * WN + 16 * j + (lane & 15); }
+  static __device__ __forceinline__ int col(int wave, int j, int lane) {
+    return (wave % T::WAVES_N) * T::WN + 16 * j + (lane & 15);
+  }
 };
 
-// One workgroup per compute unit (64-72 KB of LDS, 2 waves per SIMD). The
-// pipeline per K slice s:
+// Big: one workgroup per compute unit (64-72 KB of LDS, 2 waves per SIMD);
+// Small: two (two waves per SIMD as well). The pipeline per K slice s:
 //   - global loads of slice s+2 into registers, issued first;
-//   - 128 MFMAs per wave on the fragments of slice s, already in registers;
+//   - FM x FN x 4 MFMAs per wave on the fragments of slice s, already in
+//     registers;
 //     after the 16 MFMAs of A fragment i, that register is refilled with
 //     fragment i of slice s+1 from LDS (B fragments are double-buffered and
 //     refilled after A fragments 0-3), so LDS reads overlap the matrix pipe
 //     instead of stalling each slice start;
-//   - after the MFMAs of fragment 5, slice s+2 goes from registers to the LDS
-//     buffer that held slice s (all waves read it during slice s-1);
+//   - after the MFMAs of fragment FM - 3, slice s+2 goes from registers to the
+//     LDS buffer that held slice s (all waves read it during slice s-1);
 //   - one barrier.
 // STREAM_K = false: workgroup b computes whole tile xcd_major(b). true:
 // workgroup b is stream-K worker xcd_major(b) and computes its run, at most
 // the end of one tile and the start of the next (kept out of the whole-tile
 // kernel: the second inlined piece measurably slows the main loop).
-template <int MODE, bool STREAM_K, bool TA, bool TB>
-__global__ __launch_bounds__(kThreads, 1) void kernel(const float* __restrict__ A, const float* __restrict__ B,
-                                                      float* __restrict__ C, int64_t M, int64_t N, int64_t K,
-                                                      BatchDesc bd, TileMap tmap, Split sp) {
+template <class CFG, int MODE, bool STREAM_K, bool TA, bool TB>
+__global__ __launch_bounds__(CFG::kThreads, CFG::kMinBlocks) void kernel(const float* __restrict__ A,
+                                                                         const float* __restrict__ B,
+                                                                         float* __restrict__ C, int64_t M, int64_t N,
+                                                                         int64_t K, BatchDesc bd, TileMap tmap,
+                                                                         Split sp) {
+  constexpr int BM = CFG::BM, BN = CFG::BN, WM = CFG::WM, WN = CFG::WN, FM = CFG::FM, FN = CFG::FN;
+  constexpr int kThreads = CFG::kThreads;
+  using L = Layout<CFG>;
   constexpr int SA = lds_stride<TA>(), SB = lds_stride<!TB>();
-  __shared__ __attribute__((aligned(16))) float As[2][BM * SA];
-  __shared__ __attribute__((aligned(16))) float Bs[2][BN * SB];
+  // Double-buffered slices, one LDS variable per buffer and operand.
+  __shared__ __attribute__((aligned(16))) float As0[BM * SA];
+  __shared__ __attribute__((aligned(16))) float As1[BM * SA];
+  __shared__ __attribute__((aligned(16))) float Bs0[BN * SB];
+  __shared__ __attribute__((aligned(16))) float Bs1[BN * SB];
 
   const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
-  const int wm = wave >> 2, wn = wave & 3;
+  const int wm = wave / CFG::WAVES_N, wn = wave % CFG::WAVES_N;
 
   // Global -> register -> LDS operand slices. A is k-contiguous ([m][k])
   // unless TA ([k][m]); B is row-contiguous ([k][n]) unless TB ([n][k]).
   // k-contiguous operands go straight to LDS (DmaLoader; register-staged in
   // mode 2), K-strided ones as 2 float4 row vectors per thread (PairLoader).
-  Loader<TA, MODE> la;
-  Loader<!TB, MODE> lb;
+  Loader<TA, MODE, BM, kThreads> la;
+  Loader<!TB, MODE, BN, kThreads> lb;
   constexpr bool kDirect = decltype(la)::kDirect || decltype(lb)::kDirect;
   la.init(tid);
   lb.init(tid);
@@ -485,15 +517,15 @@ __global__ __launch_bounds__(kThreads, 1) void kernel(const float* __restrict__ 
     // apart), so the staged commit waits for them anyway; issued first they
     // have the most time. Same-box A/B at 8192^3: direct first 89.8-90.1% of
     // peak, staged first 84.6%, no direct loads 88.6-89.2%.
-    auto load_slice = [&](int64_t k0, int buf) {
-      if (decltype(la)::kDirect) la.issue(Ap, ms, M, lda, kp, k0, As[buf]);
-      if (decltype(lb)::kDirect) lb.issue(Bp, ns, N, ldb, kp, k0, Bs[buf]);
-      if (!decltype(la)::kDirect) la.issue(Ap, ms, M, lda, kp, k0, As[buf]);
-      if (!decltype(lb)::kDirect) lb.issue(Bp, ns, N, ldb, kp, k0, Bs[buf]);
+    auto load_slice = [&](int64_t k0, float* as, float* bs) {
+      if (decltype(la)::kDirect) la.issue(Ap, ms, M, lda, kp, k0, as);
+      if (decltype(lb)::kDirect) lb.issue(Bp, ns, N, ldb, kp, k0, bs);
+      if (!decltype(la)::kDirect) la.issue(Ap, ms, M, lda, kp, k0, as);
+      if (!decltype(lb)::kDirect) lb.issue(Bp, ns, N, ldb, kp, k0, bs);
     };
-    auto store_slice = [&](int buf) {
-      la.commit(As[buf]);
-      lb.commit(Bs[buf]);
+    auto store_slice = [&](float* as, float* bs) {
+      la.commit(as);
+      lb.commit(bs);
     };
     auto publish = [&] {
       if (kDirect) __builtin_amdgcn_s_waitcnt(kWaitVmcnt0);
@@ -506,28 +538,24 @@ __global__ __launch_bounds__(kThreads, 1) void kernel(const float* __restrict__ 
 #pragma unroll
       for (int j = 0; j < FN; ++j) acc[i][j] = hpd::f32x4{0.f, 0.f, 0.f, 0.f};
 
-    load_slice(0, 0);
-    store_slice(0);
+    load_slice(0, As0, Bs0);
+    store_slice(As0, Bs0);
     if (slices > 1) {
-      load_slice(BK, 1);
-      store_slice(1);
+      load_slice(BK, As1, Bs1);
+      store_slice(As1, Bs1);
     }
     publish();
     hpd::f32x4 a[FM], b[FN], b_next[FN];
 #pragma unroll
-    for (int i = 0; i < FM; ++i) a[i] = *reinterpret_cast<const hpd::f32x4*>(&As[0][a_read + 16 * i * SA]);
+    for (int i = 0; i < FM; ++i) a[i] = *reinterpret_cast<const hpd::f32x4*>(&As0[a_read + 16 * i * SA]);
 #pragma unroll
-    for (int j = 0; j < FN; ++j) b[j] = *reinterpret_cast<const hpd::f32x4*>(&Bs[0][b_read + 16 * j * SB]);
-    __syncthreads();  // every wave has read buffer 0 before slice 0 refills it
-    // Fragment read addresses of the next slice, carried across iterations:
-    // indexing As[(s + 1) & 1] directly lets the compiler rematerialize the
-    // address into each fragment register, and that write has to wait for
-    // the MFMAs still reading the register (measured: -3% of peak).
-    const float* a_src = &As[1][a_read];
-    const float* b_src = &Bs[1][b_read];
-    for (int64_t s = 0; s < slices; ++s) {
+    for (int j = 0; j < FN; ++j) b[j] = *reinterpret_cast<const hpd::f32x4*>(&Bs0[b_read + 16 * j * SB]);
+    // Slice s: slice s+2 goes into the buffers (as, bs) that held slice s,
+    // fragments of slice s+1 come from an, bn (buffer plus this lane's
+    // fragment offset).
+    auto slice = [&](int64_t s, float* as, float* bs, const float* an, const float* bn) {
       const bool more = s + 1 < slices;
-      if (s + 2 < slices) load_slice((s + 2) * BK, int(s & 1));
+      if (s + 2 < slices) load_slice((s + 2) * BK, as, bs);
 #pragma unroll
       for (int i = 0; i < FM; ++i) {
 #pragma unroll
@@ -536,18 +564,40 @@ __global__ __launch_bounds__(kThreads, 1) void kernel(const float* __restrict__ 
           for (int j = 0; j < FN; ++j)
             acc[i][j] = __builtin_amdgcn_mfma_f32_16x16x4f32(a[i][q], b[j][q], acc[i][j], 0, 0, 0);
         if (more) {
-          a[i] = *reinterpret_cast<const hpd::f32x4*>(a_src + 16 * i * SA);
+          a[i] = *reinterpret_cast<const hpd::f32x4*>(an + 16 * i * SA);
           // B refills ride on the first FN A fragments, so only A refills
           // are in flight at the barrier (same-box A/B: +0.3-0.6% of peak).
-          if (i < FN) b_next[i] = *reinterpret_cast<const hpd::f32x4*>(b_src + 16 * i * SB);
+          if (i < FN) b_next[i] = *reinterpret_cast<const hpd::f32x4*>(bn + 16 * i * SB);
         }
-        if (i == 5 && s + 2 < slices) store_slice(int(s & 1));
+        if (i == CFG::kCommitAfter && s + 2 < slices) store_slice(as, bs);
       }
 #pragma unroll
       for (int j = 0; j < FN; ++j) b[j] = b_next[j];
-      a_src = (s & 1) ? &As[1][a_read] : &As[0][a_read];
-      b_src = (s & 1) ? &Bs[1][b_read] : &Bs[0][b_read];
       publish();
+    };
+    // Every wave has read buffer 0 before slice 0 refills it. This barrier
+    // sits under the loop's own guard (slices > 0 always holds). Before the
+    // guard, the compiler sank the reads above to their first use, past the
+    // barrier, where a late wave could read slice 2's data after a faster
+    // wave's LDS-DMA refilled buffer 0 (one wrong 16 x 64 fragment block,
+    // with several workgroups per compute unit). Other ways of holding the
+    // reads above the barrier (an asm memory clobber, an asm use of the
+    // fragments, buffer arrays indexed at run time) led the compiler to wait
+    // for vmcnt(0) before every fragment read of the loop (8192^3: -4% of
+    // peak), and so did unrolling two slices per iteration over fixed
+    // buffers (-2.5%). The assembly is checked for both in the CPU tests.
+    if (slices > 0) __syncthreads();
+    // The next slice's fragment addresses are carried across iterations:
+    // picking them per slice lets the compiler rematerialize the address
+    // into each fragment register, and that write has to wait for the MFMAs
+    // still reading the register (measured: -3% of peak).
+    const float* an = As1 + a_read;
+    const float* bn = Bs1 + b_read;
+    for (int64_t s = 0; s < slices; ++s) {
+      const bool odd = s & 1;
+      slice(s, odd ? As1 : As0, odd ? Bs1 : Bs0, an, bn);
+      an = (odd ? As1 : As0) + a_read;
+      bn = (odd ? Bs1 : Bs0) + b_read;
     }
 
     if (slot < 0) {
@@ -556,10 +606,10 @@ __global__ __launch_bounds__(kThreads, 1) void kernel(const float* __restrict__ 
       for (int i = 0; i < FM; ++i) {
 #pragma unroll
         for (int j = 0; j < FN; ++j) {
-          const int64_t col = ns + Layout::col(wave, j, lane);
+          const int64_t col = ns + L::col(wave, j, lane);
 #pragma unroll
           for (int r = 0; r < 4; ++r) {
-            const int64_t row = ms + Layout::row(wave, i, lane, r);
+            const int64_t row = ms + L::row(wave, i, lane, r);
             if (MODE == 0 || (row >= m0 && row < M && col >= n0 && col < N)) Cb[row * tmap.ldc + col] = acc[i][j][r];
           }
         }
@@ -686,8 +736,11 @@ template <int MODE, bool STREAM_K, bool TA, bool TB>
 __global__ __launch_bounds__(kThreads, 1) void kernel(const double* __restrict__ A, const double* __restrict__ B,
                                                       double* __restrict__ C, int64_t M, int64_t N, int64_t K,
                                                       BatchDesc bd, TileMap tmap, Split sp) {
-  __shared__ __attribute__((aligned(16))) double As[2][BM * S];
-  __shared__ __attribute__((aligned(16))) double Bs[2][BN * S];
+  // Double-buffered slices, one LDS variable per buffer and operand.
+  __shared__ __attribute__((aligned(16))) double As0[BM * S];
+  __shared__ __attribute__((aligned(16))) double As1[BM * S];
+  __shared__ __attribute__((aligned(16))) double Bs0[BN * S];
+  __shared__ __attribute__((aligned(16))) double Bs1[BN * S];
 
   const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
   const int wm = wave >> 1, wn = wave & 1;
@@ -725,15 +778,15 @@ __global__ __launch_bounds__(kThreads, 1) void kernel(const double* __restrict__
     // called through SliceLoader::load itself: at the 256-VGPR limit of the
     // all-staged mode-2 kernels, one more inlined wrapper level reshuffled
     // registers into spills (transposed A: 23 -> 209 spilled VGPRs).
-    auto load_slice = [&](int64_t k0, int buf) {
-      if constexpr (decltype(la)::kDirect) la.issue(Ap, m0, M, lda, kp, k0, As[buf]);
-      if constexpr (decltype(lb)::kDirect) lb.issue(Bp, n0, N, ldb, kp, k0, Bs[buf]);
+    auto load_slice = [&](int64_t k0, double* as, double* bs) {
+      if constexpr (decltype(la)::kDirect) la.issue(Ap, m0, M, lda, kp, k0, as);
+      if constexpr (decltype(lb)::kDirect) lb.issue(Bp, n0, N, ldb, kp, k0, bs);
       if constexpr (!decltype(la)::kDirect) la.load(Ap, m0, M, lda, kp, k0);
       if constexpr (!decltype(lb)::kDirect) lb.load(Bp, n0, N, ldb, kp, k0);
     };
-    auto store_slice = [&](int buf) {
-      la.commit(As[buf]);
-      lb.commit(Bs[buf]);
+    auto store_slice = [&](double* as, double* bs) {
+      la.commit(as);
+      lb.commit(bs);
     };
     auto publish = [&] {
       if (kDirect) __builtin_amdgcn_s_waitcnt(kWaitVmcnt0);
@@ -746,31 +799,28 @@ __global__ __launch_bounds__(kThreads, 1) void kernel(const double* __restrict__
 #pragma unroll
       for (int j = 0; j < FN; ++j) acc[i][j] = f64x4{0.0, 0.0, 0.0, 0.0};
 
-    load_slice(0, 0);
-    store_slice(0);
+    load_slice(0, As0, Bs0);
+    store_slice(As0, Bs0);
     if (slices > 1) {
-      load_slice(BK, 1);
-      store_slice(1);
+      load_slice(BK, As1, Bs1);
+      store_slice(As1, Bs1);
     }
     publish();
     hpd::f64x2 a[2][FM], b[2][FN];
 #pragma unroll
     for (int i = 0; i < FM; ++i) {
-      a[0][i] = *reinterpret_cast<const hpd::f64x2*>(&As[0][a_read0 + 16 * i * S]);
-      a[1][i] = *reinterpret_cast<const hpd::f64x2*>(&As[0][a_read1 + 16 * i * S]);
+      a[0][i] = *reinterpret_cast<const hpd::f64x2*>(&As0[a_read0 + 16 * i * S]);
+      a[1][i] = *reinterpret_cast<const hpd::f64x2*>(&As0[a_read1 + 16 * i * S]);
     }
 #pragma unroll
     for (int j = 0; j < FN; ++j) {
-      b[0][j] = *reinterpret_cast<const hpd::f64x2*>(&Bs[0][b_read0 + 16 * j * S]);
-      b[1][j] = *reinterpret_cast<const hpd::f64x2*>(&Bs[0][b_read1 + 16 * j * S]);
+      b[0][j] = *reinterpret_cast<const hpd::f64x2*>(&Bs0[b_read0 + 16 * j * S]);
+      b[1][j] = *reinterpret_cast<const hpd::f64x2*>(&Bs0[b_read1 + 16 * j * S]);
     }
-    __syncthreads();  // every wave has read buffer 0 before slice 0 refills it
-    // Next-slice LDS buffers, carried across iterations (see the fp32 kernel).
-    const double* a_src = As[1];
-    const double* b_src = Bs[1];
-    for (int64_t s = 0; s < slices; ++s) {
+    // Slice s as in the fp32 kernel: into (as, bs), fragments from (an, bn).
+    auto slice = [&](int64_t s, double* as, double* bs, const double* an, const double* bn) {
       const bool more = s + 1 < slices;
-      if (s + 2 < slices) load_slice((s + 2) * BK, int(s & 1));
+      if (s + 2 < slices) load_slice((s + 2) * BK, as, bs);
 #pragma unroll
       for (int h = 0; h < 2; ++h) {
         const int a_read = h == 0 ? a_read0 : a_read1;
@@ -782,17 +832,26 @@ __global__ __launch_bounds__(kThreads, 1) void kernel(const double* __restrict__
 #pragma unroll
             for (int j = 0; j < FN; ++j)
               acc[i][j] = __builtin_amdgcn_mfma_f64_16x16x4f64(a[h][i][q], b[h][j][q], acc[i][j], 0, 0, 0);
-          if (more) a[h][i] = *reinterpret_cast<const hpd::f64x2*>(a_src + a_read + 16 * i * S);
+          if (more) a[h][i] = *reinterpret_cast<const hpd::f64x2*>(an + a_read + 16 * i * S);
         }
         if (more) {
 #pragma unroll
-          for (int j = 0; j < FN; ++j) b[h][j] = *reinterpret_cast<const hpd::f64x2*>(b_src + b_read + 16 * j * S);
+          for (int j = 0; j < FN; ++j) b[h][j] = *reinterpret_cast<const hpd::f64x2*>(bn + b_read + 16 * j * S);
         }
-        if (h == 0 && s + 2 < slices) store_slice(int(s & 1));
+        if (h == 0 && s + 2 < slices) store_slice(as, bs);
       }
-      a_src = (s & 1) ? As[1] : As[0];
-      b_src = (s & 1) ? Bs[1] : Bs[0];
       publish();
+    };
+    // Every wave has read buffer 0 before slice 0 refills it: the barrier
+    // under the loop's guard, and the carried buffers, as in the fp32 kernel.
+    if (slices > 0) __syncthreads();
+    const double* an = As1;
+    const double* bn = Bs1;
+    for (int64_t s = 0; s < slices; ++s) {
+      const bool odd = s & 1;
+      slice(s, odd ? As1 : As0, odd ? Bs1 : Bs0, an, bn);
+      an = odd ? As1 : As0;
+      bn = odd ? Bs1 : Bs0;
     }
 
     if (slot < 0) {
@@ -969,29 +1028,58 @@ bool dma_aligned(const T* a, const T* b, const BatchDesc& bd) {
   return (TA || aligned(a, bd.a_stride)) && (!TB || aligned(b, bd.b_stride));
 }
 
-// The tiled MFMA product over an m x n block whose B and C rows are ldb and
-// ldc elements long.
-template <bool TA, bool TB>
-void run_f32_tiles(hp_ctx* ctx, const float* a, const float* b, float* c, int64_t m, int64_t n, int64_t k,
-                   const BatchDesc& bd, int64_t batch, int64_t lda, int64_t ldb, int64_t ldc) {
+// The tiled MFMA product over an m x n block with one tile configuration.
+template <class CFG, bool TA, bool TB>
+void run_f32_config(hp_ctx* ctx, const float* a, const float* b, float* c, int64_t m, int64_t n, int64_t k,
+                    const BatchDesc& bd, int64_t batch, int64_t lda, int64_t ldb, int64_t ldc) {
   using namespace f32;
+  constexpr int BM = CFG::BM, BN = CFG::BN, T = CFG::kThreads;
   TileMap tm;
   prepare(m, n, batch, BM, BN, tm, lda, ldb, ldc);
-  auto fix = fixup_kernel<float, hpd::f32x4, Layout>;
+  auto fix = fixup_kernel<float, hpd::f32x4, Layout<CFG>>;
   int mode = mode_of(m, n, k, BM, BN, BK);
   if (!dma_aligned<float, TA, TB>(a, b, bd)) mode = 2;
   switch (mode) {
     case 0:
-      launch_split<float, BM, BN>(ctx, kernel<0, false, TA, TB>, kernel<0, true, TA, TB>, fix, kThreads, a, b, c, m,
-                                  n, k, bd, tm, BK, "gemm_f32", false);
+      launch_split<float, BM, BN>(ctx, kernel<CFG, 0, false, TA, TB>, kernel<CFG, 0, true, TA, TB>, fix, T, a, b, c,
+                                  m, n, k, bd, tm, BK, "gemm_f32", false);
       break;
     case 1:
-      launch_split<float, BM, BN>(ctx, kernel<1, false, TA, TB>, kernel<1, true, TA, TB>, fix, kThreads, a, b, c, m,
-                                  n, k, bd, tm, BK, "gemm_f32", true);
+      launch_split<float, BM, BN>(ctx, kernel<CFG, 1, false, TA, TB>, kernel<CFG, 1, true, TA, TB>, fix, T, a, b, c,
+                                  m, n, k, bd, tm, BK, "gemm_f32", true);
       break;
     default:
-      launch_split<float, BM, BN>(ctx, kernel<2, false, TA, TB>, kernel<2, true, TA, TB>, fix, kThreads, a, b, c, m,
-                                  n, k, bd, tm, BK, "gemm_f32", true);
+      launch_split<float, BM, BN>(ctx, kernel<CFG, 2, false, TA, TB>, kernel<CFG, 2, true, TA, TB>, fix, T, a, b, c,
+                                  m, n, k, bd, tm, BK, "gemm_f32", true);
+  }
+}
+
+// Tile choice. Big unless its tiles fill less than two rounds of the chip,
+// leave the last one partly filled (stream-K then cuts them) and the product
+// is short: at most 64 K slices, or at most a quarter round of tiles and 256
+// slices. Small has four times the tiles at three workgroups per compute
+// unit but moves twice the operand bytes per flop, so it loses where Big
+// runs whole rounds (4096 x 4096 x 1024: 114 against 133 TFLOP/s) and where
+// stream-K runs are long. Measured on one MI355X, TFLOP/s Big / Small:
+//   1024^3 42 / 62, 1536^3 85 / 90, 1024 x 1024 x 4096 94 / 97,
+//   64 x (512 x 1024 @ 1024 x 768) 124 / 128, 6144 x 4096 x 1024 124 / 128;
+//   1024 x 1024 x 16384 124 / 121, 6144 x 4096 x 2048 132 / 131,
+//   4097 x 3001 x 2049 113 / 109, 8192 x 1024 x 4096 130 / 124.
+inline bool small_tiles(hp_ctx* ctx, int64_t m, int64_t n, int64_t k, int64_t batch) {
+  using f32::Big;
+  const int64_t tiles = hp::ceil_div(m, Big::BM) * hp::ceil_div(n, Big::BN) * batch;
+  const int64_t cus = ctx->compute_units, slices = hp::ceil_div(k, f32::BK);
+  if (tiles >= 2 * cus || tiles % cus == 0) return false;
+  return slices <= 64 || (4 * tiles <= cus && slices <= 256);
+}
+
+template <bool TA, bool TB>
+void run_f32_tiles(hp_ctx* ctx, const float* a, const float* b, float* c, int64_t m, int64_t n, int64_t k,
+                   const BatchDesc& bd, int64_t batch, int64_t lda, int64_t ldb, int64_t ldc) {
+  if (small_tiles(ctx, m, n, k, batch)) {
+    run_f32_config<f32::Small, TA, TB>(ctx, a, b, c, m, n, k, bd, batch, lda, ldb, ldc);
+  } else {
+    run_f32_config<f32::Big, TA, TB>(ctx, a, b, c, m, n, k, bd, batch, lda, ldb, ldc);
   }
 }
 
@@ -1005,8 +1093,7 @@ void run_f32_tiles(hp_ctx* ctx, const float* a, const float* b, float* c, int64_
 template <bool TA, bool TB>
 void run_f32(hp_ctx* ctx, const float* a, const float* b, float* c, int64_t m, int64_t n, int64_t k,
              const BatchDesc& bd, int64_t batch) {
-  using f32::BM;
-  using f32::BN;
+  constexpr int64_t BM = f32::Big::BM, BN = f32::Big::BN;
   const int64_t lda = TA ? m : k, ldb = TB ? k : n;
   if (batch == 1) {
     const int64_t rows = m % BM, cols = n % BN;

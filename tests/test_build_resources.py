@@ -8,6 +8,8 @@ than any test of results shows (a spilling fp64 GEMM loader once cost
 are checked here: no fp32 GEMM, GEMV, norm, reduction or RNG kernel spills,
 fp64 GEMM kernels stay within their known spills, and the GEMMs keep two
 waves per SIMD. Skipped when the library has not been built in this tree.
+The GEMM units are also compiled to assembly here, to check the order of
+their LDS reads, barriers and waits.
 """
 
 import json
@@ -61,3 +63,51 @@ def test_streaming_kernels_do_not_spill(resources, unit):
     for name, r in kernels.items():
         assert r.get("VGPRs Spill", 0) == 0 and r.get("SGPRs Spill", 0) == 0, (unit, name, r)
         assert r.get("Dynamic Stack") in (None, "False"), (unit, name, r)
+
+
+# Two properties of the GEMM kernels' assembly that no result test sees:
+# 1. The prologue reads LDS buffer 0 between the first two barriers; the
+#    second orders those reads before slice 2's LDS writes into the same
+#    buffer. If the compiler sinks the reads below it (into the block that
+#    first uses them), a late wave can read slice 2's data (seen as one wrong
+#    16 x 64 fragment block in batched products with several workgroups per
+#    compute unit).
+# 2. No fragment read waits for vmcnt: the LDS-DMA in flight during a slice
+#    writes the other buffer. A wait there (the compiler adds one for some
+#    placements of that barrier) cost 8192^3 4% of peak.
+@pytest.mark.parametrize("unit", [f"gemm_{t}_{layout}" for t in ("f32", "f64") for layout in ("nn", "nt", "tn", "tt")])
+def test_gemm_lds_reads_keep_their_barriers_and_skip_dma_waits(unit, tmp_path):
+    import importlib.util
+    import shutil
+    import subprocess
+
+    spec = importlib.util.spec_from_file_location("pacho_build", RESOURCES.parents[1] / "build.py")
+    build = importlib.util.module_from_spec(spec)
+    spec.loader.exec_module(build)
+    if not (shutil.which("hipcc") or Path("/opt/rocm/bin/hipcc").exists()):
+        pytest.skip("hipcc not available")
+    source = build.CSRC / f"{unit}.hip"
+    asm = tmp_path / f"{unit}.s"
+    flags = [f for f in build.FLAGS if f != "-Wall"]
+    subprocess.run([build.hipcc(), *flags, "--cuda-device-only", "-S", str(source), "-o", str(asm)], check=True,
+                   capture_output=True)
+    kernel, previous, barriers, checked = None, "", {}, set()
+    for line in asm.read_text().splitlines():
+        text = line.strip()
+        if line.startswith("_Z") and ":" in line:  # a function label
+            kernel = line.split(":")[0]
+            barriers[kernel] = []
+        if kernel is None or not text or text.startswith(";"):
+            continue
+        if text.startswith("s_barrier"):
+            barriers[kernel].append(0)
+        elif text.startswith("ds_read") and barriers[kernel]:
+            barriers[kernel][-1] += 1  # LDS reads after the latest barrier
+        if text.startswith("ds_read"):
+            assert not previous.startswith("s_waitcnt vmcnt"), f"fragment read waits for vmcnt in {kernel}"
+        previous = text
+    for kernel, reads in barriers.items():
+        if "kernel" in kernel and len(reads) >= 2:
+            checked.add(kernel)
+            assert reads[0] > 0, f"no LDS reads between the first two barriers (sunk reads) in {kernel}"
+    assert checked, unit

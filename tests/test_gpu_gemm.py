@@ -132,11 +132,16 @@ def test_kernel_modes_against_float64(hip, dtype, m, n, k):
     assert np.all(np.abs(got - want) <= bound * scale + 1e-30)
 
 
-# Tile counts that leave the last round of resident workgroups (one per
-# compute unit) partly filled, so their K slices are cut into stream-K runs
-# and summed by the fixup kernel: runs that cross tile boundaries (extra > 0),
-# single-tile problems cut over many workers, batched tiles, every load mode.
+# Tile counts that leave the last round of resident workgroups partly
+# filled, so their K slices are cut into stream-K runs and summed by the fixup
+# kernel: runs that cross tile boundaries (extra > 0), single-tile problems
+# cut over many workers, batched tiles, every load mode. Products of at most
+# 256 K slices take the 128 x 128 tiles (three workgroups per compute unit),
+# longer ones the 256 x 256 tiles (one per compute unit): both are covered.
 STREAM_K_CASES = [
+    (np.float32, (), 512, 256, 8192),  # 256 x 256 tiles: interior, 2 tiles x 512 slices
+    (np.float32, (), 1000, 700, 4100),  # 256 x 256 tiles: edges, K % 16 == 4
+    (np.float32, (2,), 600, 300, 4096),  # 256 x 256 tiles: batched, moved edge tiles
     (np.float32, (), 512, 256, 1552),  # interior, 2 tiles x 97 slices
     (np.float32, (), 31, 33, 4099),  # one tile cut over 32 workers
     (np.float32, (), 1000, 700, 2000),  # M/N edges, 12 tiles
@@ -275,8 +280,15 @@ def test_config4_batched_broadcast(hip):
     rng = np.random.default_rng(3)
     a = rng.uniform(-1, 1, (64, 512, 1024)).astype(np.float32)
     b = rng.uniform(-1, 1, (1024, 768)).astype(np.float32)
-    got = p.asnumpy(p.asarray(a, backend=hip) @ p.asarray(b, backend=hip))
+    A, B = p.asarray(a, backend=hip), p.asarray(b, backend=hip)
+    got = p.asnumpy(A @ B)
     assert got.shape == (64, 512, 768)
+    # Every batch against float32 BLAS (a wrong fragment block in any tile
+    # shows as errors of order 1), then repeated bit for bit: several
+    # workgroups share each compute unit here, which once exposed an LDS
+    # read/write race that hit different tiles on each run.
+    np.testing.assert_allclose(got, np.matmul(a, b), rtol=0, atol=1e-3)
+    np.testing.assert_array_equal(p.asnumpy(A @ B), got)
     for batch in (0, 31, 63):
         want = a[batch].astype(np.float64) @ b.astype(np.float64)
         np.testing.assert_allclose(got[batch], want, rtol=0, atol=2e-4)
