@@ -291,11 +291,16 @@ using Big = Tile<256, 256, 2, 4, 1>;
 // the tiles of Big, for products whose Big tiles do not fill the chip.
 using Small = Tile<128, 128, 2, 2, 2>;
 
+// gfx950 LDS banks, measured with SQ_LDS_BANK_CONFLICT on probe kernels: a
+// ds_read_b128 serves its 64 lanes in four groups of 16 (lane bit 5 and the
+// parity of lane bits 2-4), ds_read_b64 in two groups of 32 consecutive
+// lanes, ds_write_b64 in groups of 16 and ds_write_b128 in groups of 8; a
+// group takes as many cycles as the most distinct addresses that fall on one
+// bank set (16 bytes, 256 bytes of banks), and lanes at one address share.
+//
 // LDS rows hold 4 quads of 4 consecutive k values; quad q of row r is stored
-// at slot q ^ ((r >> 1) & 3). Rows are 16 floats (64 B), so a ds_read_b128 by
-// lanes reading rows r0..r0+15 at one logical quad, a ds_write_b128 of 4 rows x
-// 4 quads, and the B writes of 16 consecutive n at one quad all land on
-// distinct banks (measured: removes the LDS bank conflicts of padded rows).
+// at slot q ^ ((r >> 1) & 3). Rows are 16 floats (64 B); the fragment reads
+// (rows r0..r0+15, quad lane / 16) are conflict-free.
 __device__ __forceinline__ int swizzle(int row) { return (row >> 1) & 3; }
 
 // An operand whose K axis is strided in memory (B stored [k][n], or A stored
@@ -303,10 +308,12 @@ __device__ __forceinline__ int swizzle(int row) { return (row >> 1) & 3; }
 // each thread loads a 2 (k) x 4 (row) block, k = 2 kh + {0, 1} (kh = t % 8),
 // rows 4 b .. 4 b + 3 (b = t / 8), two global_load_dwordx4 instead of eight
 // scalar loads, and writes it transposed, 8 bytes per row, into LDS rows of
-// 16 k values padded to PS floats. The 80-byte row stride keeps both these
-// writes (32 lanes: 4 row blocks x 8 k pairs) and the fragment reads (16
-// consecutive rows) on distinct banks. Measured on one box: 8192^3 85.6% ->
-// 89.0% of peak, 4096^3 83.8% -> 88.1%.
+// 16 k values padded to PS floats (8192^3: 85.6% -> 89.0% of peak against
+// scalar loads). With the 80-byte row stride the commit's ds_write2_b64 (rows
+// e, e + 1) is conflict-free and each fragment read costs 4 conflict cycles;
+// no padded stride frees both (the reads need a stride of 2 mod 4 16-byte
+// units, the paired writes an odd one). Where the operand's rows are 16-byte
+// aligned, the 256-wide tiles take RowDmaLoader instead (no conflicts).
 constexpr int PS = 20;
 
 template <int ROWS, int THREADS, int MODE>
@@ -411,6 +418,59 @@ struct StagedLoader : SliceLoader<float, ROWS, false, MODE, THREADS> {
   static constexpr bool kDirect = false;
 };
 
+// A K-strided operand ([k][rows] in memory: B, or A transposed) in modes 0
+// and 1 when each of its k rows starts 16-byte aligned (host check): one
+// LDS-DMA per k row moves the tile's ROWS floats (1 KB) into LDS, stored
+// [k][row] at a row stride of RS floats. No registers, no ds_write and no
+// wait in the middle of the slice, against the register-staged pair loader
+// (8192^3: the staged B path costs 3.7% of peak, its DMA 1%). A fragment is
+// then four 4-byte reads, rows 4 (lane / 16) + q: the 16-byte pad puts the
+// four lane groups on disjoint bank sets (4 RS = 1040 dwords = 16 mod 64).
+template <int ROWS, int THREADS>
+struct RowDmaLoader {
+  static_assert(ROWS * 4 == 1024, "one 1 KB LDS-DMA per k row");
+  static constexpr int kRowsPerWave = 16 / (THREADS / 64);
+  static_assert(kRowsPerWave * (THREADS / 64) == 16, "whole k rows per wave");
+  static constexpr int RS = ROWS + 4;
+  static constexpr int kBufFloats = 16 * RS;
+  int k0w, lane;
+
+  __device__ __forceinline__ void init(int tid) {
+    k0w = kRowsPerWave * __builtin_amdgcn_readfirstlane(tid >> 6);
+    lane = tid & 63;
+  }
+
+  __device__ __forceinline__ void issue(const float* p, int64_t r0, int64_t, int64_t ld, int64_t, int64_t k0,
+                                        float* buf) const {
+#pragma unroll
+    for (int i = 0; i < kRowsPerWave; ++i) {
+      const int k = k0w + i;
+      const float* src = p + (k0 + k) * ld + r0 + 4 * lane;
+      __builtin_amdgcn_global_load_lds(static_cast<const void*>(src),
+                                       (__attribute__((address_space(3))) void*)(buf + k * RS), 16, 0, 0);
+    }
+  }
+  __device__ __forceinline__ void commit(float*) const {}
+  static constexpr bool kDirect = true;
+
+  __device__ __forceinline__ static int64_t origin(int64_t s0, int64_t ld) { return s0 * 16 * ld; }
+  // Fragment base of lane `lane` for tile rows row0 + (lane & 15).
+  __device__ __forceinline__ static int read_offset(int row0, int lane) {
+    return 4 * (lane >> 4) * RS + row0 + (lane & 15);
+  }
+  // Fragment `f` (rows 16 f on): k values 4 (lane / 16) + q, q = 0..3.
+  __device__ __forceinline__ static hpd::f32x4 read(const float* base, int f) {
+    return hpd::f32x4{base[16 * f], base[16 * f + RS], base[16 * f + 2 * RS], base[16 * f + 3 * RS]};
+  }
+};
+
+// LDS floats per buffer: the row-DMA layout's, else ROWS x the row stride.
+template <class L, bool ROW, int FALLBACK>
+constexpr int buf_floats() {
+  if constexpr (ROW) return L::kBufFloats;
+  else return FALLBACK;
+}
+
 // LDS row stride of an operand and its loader: k-contiguous operands use the
 // swizzled 16-float rows of SliceLoader, K-strided ones the padded pair rows.
 template <bool KM>
@@ -461,7 +521,7 @@ struct Layout {
 // workgroup b is stream-K worker xcd_major(b) and computes its run, at most
 // the end of one tile and the start of the next (kept out of the whole-tile
 // kernel: the second inlined piece measurably slows the main loop).
-template <class CFG, int MODE, bool STREAM_K, bool TA, bool TB>
+template <class CFG, int MODE, bool STREAM_K, bool TA, bool TB, bool ROWDMA>
 __global__ __launch_bounds__(CFG::kThreads, CFG::kMinBlocks) void kernel(const float* __restrict__ A,
                                                                          const float* __restrict__ B,
                                                                          float* __restrict__ C, int64_t M, int64_t N,
@@ -471,11 +531,16 @@ __global__ __launch_bounds__(CFG::kThreads, CFG::kMinBlocks) void kernel(const f
   constexpr int kThreads = CFG::kThreads;
   using L = Layout<CFG>;
   constexpr int SA = lds_stride<TA>(), SB = lds_stride<!TB>();
+  // ROWDMA: K-strided operands (A if TA, B unless TB) arrive by RowDmaLoader.
+  constexpr bool kRowA = TA && ROWDMA && MODE != 2, kRowB = !TB && ROWDMA && MODE != 2;
+  using LA = typename std::conditional<kRowA, RowDmaLoader<BM, kThreads>, Loader<TA, MODE, BM, kThreads>>::type;
+  using LB = typename std::conditional<kRowB, RowDmaLoader<BN, kThreads>, Loader<!TB, MODE, BN, kThreads>>::type;
+  constexpr int kBufA = buf_floats<LA, kRowA, BM * SA>(), kBufB = buf_floats<LB, kRowB, BN * SB>();
   // Double-buffered slices, one LDS variable per buffer and operand.
-  __shared__ __attribute__((aligned(16))) float As0[BM * SA];
-  __shared__ __attribute__((aligned(16))) float As1[BM * SA];
-  __shared__ __attribute__((aligned(16))) float Bs0[BN * SB];
-  __shared__ __attribute__((aligned(16))) float Bs1[BN * SB];
+  __shared__ __attribute__((aligned(16))) float As0[kBufA];
+  __shared__ __attribute__((aligned(16))) float As1[kBufA];
+  __shared__ __attribute__((aligned(16))) float Bs0[kBufB];
+  __shared__ __attribute__((aligned(16))) float Bs1[kBufB];
 
   const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
   const int wm = wave / CFG::WAVES_N, wn = wave % CFG::WAVES_N;
@@ -484,16 +549,28 @@ __global__ __launch_bounds__(CFG::kThreads, CFG::kMinBlocks) void kernel(const f
   // unless TA ([k][m]); B is row-contiguous ([k][n]) unless TB ([n][k]).
   // k-contiguous operands go straight to LDS (DmaLoader; register-staged in
   // mode 2), K-strided ones as 2 float4 row vectors per thread (PairLoader).
-  Loader<TA, MODE, BM, kThreads> la;
-  Loader<!TB, MODE, BN, kThreads> lb;
+  LA la;
+  LB lb;
   constexpr bool kDirect = decltype(la)::kDirect || decltype(lb)::kDirect;
   la.init(tid);
   lb.init(tid);
   const int64_t lda = tmap.lda, ldb = tmap.ldb;
   // Rows read by a lane differ by multiples of 16, so the swizzle of every
   // row it reads equals that of (lane & 15).
-  const int a_read = fragment_offset<TA>(wm * WM, lane);
-  const int b_read = fragment_offset<!TB>(wn * WN, lane);
+  int a_read, b_read;
+  if constexpr (kRowA) a_read = LA::read_offset(wm * WM, lane);
+  else a_read = fragment_offset<TA>(wm * WM, lane);
+  if constexpr (kRowB) b_read = LB::read_offset(wn * WN, lane);
+  else b_read = fragment_offset<!TB>(wn * WN, lane);
+  // Fragment f of A (B) at base = buffer + a_read (b_read).
+  auto frag_a = [&](const float* base, int f) {
+    if constexpr (kRowA) return LA::read(base, f);
+    else return *reinterpret_cast<const hpd::f32x4*>(base + 16 * f * SA);
+  };
+  auto frag_b = [&](const float* base, int f) {
+    if constexpr (kRowB) return LB::read(base, f);
+    else return *reinterpret_cast<const hpd::f32x4*>(base + 16 * f * SB);
+  };
 
   // Tile `tile` over K slices [s0, s1). slot < 0: the piece is the whole K
   // range and is stored to C; else it goes to workspace slot `slot`.
@@ -547,9 +624,9 @@ __global__ __launch_bounds__(CFG::kThreads, CFG::kMinBlocks) void kernel(const f
     publish();
     hpd::f32x4 a[FM], b[FN], b_next[FN];
 #pragma unroll
-    for (int i = 0; i < FM; ++i) a[i] = *reinterpret_cast<const hpd::f32x4*>(&As0[a_read + 16 * i * SA]);
+    for (int i = 0; i < FM; ++i) a[i] = frag_a(As0 + a_read, i);
 #pragma unroll
-    for (int j = 0; j < FN; ++j) b[j] = *reinterpret_cast<const hpd::f32x4*>(&Bs0[b_read + 16 * j * SB]);
+    for (int j = 0; j < FN; ++j) b[j] = frag_b(Bs0 + b_read, j);
     // Slice s: slice s+2 goes into the buffers (as, bs) that held slice s,
     // fragments of slice s+1 come from an, bn (buffer plus this lane's
     // fragment offset).
@@ -564,10 +641,10 @@ __global__ __launch_bounds__(CFG::kThreads, CFG::kMinBlocks) void kernel(const f
           for (int j = 0; j < FN; ++j)
             acc[i][j] = __builtin_amdgcn_mfma_f32_16x16x4f32(a[i][q], b[j][q], acc[i][j], 0, 0, 0);
         if (more) {
-          a[i] = *reinterpret_cast<const hpd::f32x4*>(an + 16 * i * SA);
+          a[i] = frag_a(an, i);
           // B refills ride on the first FN A fragments, so only A refills
           // are in flight at the barrier (same-box A/B: +0.3-0.6% of peak).
-          if (i < FN) b_next[i] = *reinterpret_cast<const hpd::f32x4*>(bn + 16 * i * SB);
+          if (i < FN) b_next[i] = frag_b(bn, i);
         }
         if (i == CFG::kCommitAfter && s + 2 < slices) store_slice(as, bs);
       }
@@ -1028,29 +1105,49 @@ bool dma_aligned(const T* a, const T* b, const BatchDesc& bd) {
   return (TA || aligned(a, bd.a_stride)) && (!TB || aligned(b, bd.b_stride));
 }
 
+// RowDmaLoader needs every k row of its operand (A if TA, B unless TB)
+// 16-byte aligned: the base pointer and each batch stride, the leading
+// dimension, and the tile origins along the rows (multiples of the tile, or
+// extent - tile for the moved edge tiles of mode 1).
+template <bool TA, bool TB>
+bool rows_aligned(const float* a, const float* b, const BatchDesc& bd, int64_t m, int64_t n, int64_t lda,
+                  int64_t ldb) {
+  auto aligned = [&](const float* p, const int64_t* strides, int64_t ld, int64_t extent) {
+    if (reinterpret_cast<uintptr_t>(p) % 16 != 0 || ld % 4 != 0 || extent % 4 != 0) return false;
+    for (int d = 0; d < bd.rank; ++d)
+      if (strides[d] % 4 != 0) return false;
+    return true;
+  };
+  return (!TA || aligned(a, bd.a_stride, lda, m)) && (TB || aligned(b, bd.b_stride, ldb, n));
+}
+
 // The tiled MFMA product over an m x n block with one tile configuration.
 template <class CFG, bool TA, bool TB>
 void run_f32_config(hp_ctx* ctx, const float* a, const float* b, float* c, int64_t m, int64_t n, int64_t k,
                     const BatchDesc& bd, int64_t batch, int64_t lda, int64_t ldb, int64_t ldc) {
   using namespace f32;
   constexpr int BM = CFG::BM, BN = CFG::BN, T = CFG::kThreads;
+  // Row LDS-DMA takes 1 KB rows (256-wide tiles) and a K-strided operand.
+  constexpr bool kRows = BM * 4 == 1024 && BN * 4 == 1024 && (TA || !TB);
   TileMap tm;
   prepare(m, n, batch, BM, BN, tm, lda, ldb, ldc);
   auto fix = fixup_kernel<float, hpd::f32x4, Layout<CFG>>;
   int mode = mode_of(m, n, k, BM, BN, BK);
   if (!dma_aligned<float, TA, TB>(a, b, bd)) mode = 2;
-  switch (mode) {
-    case 0:
-      launch_split<float, BM, BN>(ctx, kernel<CFG, 0, false, TA, TB>, kernel<CFG, 0, true, TA, TB>, fix, T, a, b, c,
-                                  m, n, k, bd, tm, BK, "gemm_f32", false);
-      break;
-    case 1:
-      launch_split<float, BM, BN>(ctx, kernel<CFG, 1, false, TA, TB>, kernel<CFG, 1, true, TA, TB>, fix, T, a, b, c,
-                                  m, n, k, bd, tm, BK, "gemm_f32", true);
-      break;
-    default:
-      launch_split<float, BM, BN>(ctx, kernel<CFG, 2, false, TA, TB>, kernel<CFG, 2, true, TA, TB>, fix, T, a, b, c,
-                                  m, n, k, bd, tm, BK, "gemm_f32", true);
+  const bool rows = kRows && mode != 2 && rows_aligned<TA, TB>(a, b, bd, m, n, lda, ldb);
+  auto run = [&](auto whole, auto cut, bool moved) {
+    launch_split<float, BM, BN>(ctx, whole, cut, fix, T, a, b, c, m, n, k, bd, tm, BK, "gemm_f32", moved);
+  };
+  if (mode == 0 && rows) {
+    run(kernel<CFG, 0, false, TA, TB, kRows>, kernel<CFG, 0, true, TA, TB, kRows>, false);
+  } else if (mode == 0) {
+    run(kernel<CFG, 0, false, TA, TB, false>, kernel<CFG, 0, true, TA, TB, false>, false);
+  } else if (mode == 1 && rows) {
+    run(kernel<CFG, 1, false, TA, TB, kRows>, kernel<CFG, 1, true, TA, TB, kRows>, true);
+  } else if (mode == 1) {
+    run(kernel<CFG, 1, false, TA, TB, false>, kernel<CFG, 1, true, TA, TB, false>, true);
+  } else {
+    run(kernel<CFG, 2, false, TA, TB, false>, kernel<CFG, 2, true, TA, TB, false>, true);
   }
 }
 
