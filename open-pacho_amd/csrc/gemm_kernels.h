@@ -80,7 +80,8 @@ constexpr int64_t kGroupM = 8;
 // or a view at any element offset): one global_load_dwordx4 all the same.
 typedef float f32x4u __attribute__((ext_vector_type(4), aligned(4)));
 typedef double f64x2u __attribute__((ext_vector_type(2), aligned(8)));
-constexpr int64_t kMinSlices = 8;  // shortest stream-K run
+constexpr int64_t kShortRun = 8;   // shortest stream-K run
+constexpr int64_t kLongRun = 16;   // run length once every compute unit has one
 
 __device__ __forceinline__ void logical_tile(int64_t t, const TileMap& tm, int64_t& batch, int64_t& ti,
                                              int64_t& tj) {
@@ -1037,23 +1038,34 @@ int resident_per_cu(F kernel, int threads) {
   return blocks;
 }
 
-// Whole tiles for every complete round of `slots` resident workgroups; the
-// tiles of an incomplete last round go to stream-K unless that round is
-// nearly full or K is too short to cut.
-Split plan_split(int64_t total, int64_t slices, int64_t slots) {
+// Whole tiles for every complete round of cus * per_cu resident workgroups;
+// the tiles of an incomplete last round go to stream-K unless that round is
+// nearly full or K is too short to cut. Every stream-K run writes two
+// partial tiles that the fixup reads back, so fewer, longer runs can win
+// over filling every slot: runs of kLongRun slices, but each compute unit
+// one run of at least kShortRun, and at most two runs per compute unit (or
+// one per cut tile, if more). Measured on one MI355X, TFLOP/s: 128 x 128
+// tiles of 1024^3 62 / 66 / 46 with runs of 8 / 16 / 32 slices (512 / 256 /
+// 128 workers); 1024 x 1024 x 4096 96 with three workers per compute unit,
+// 104 with two; 256 x 256 tiles of 512 x 512 x 8192 56 with 256 runs of 8,
+// 52 with 128 of 16.
+Split plan_split(int64_t total, int64_t slices, int64_t cus, int64_t per_cu) {
   Split sp{};
   sp.dp_tiles = total;
   sp.slices = slices;
+  const int64_t slots = cus * per_cu;
   const int64_t rem = total % slots;
-  if (rem == 0 || 8 * rem >= 7 * slots || slices < 2 * kMinSlices) return sp;
+  if (rem == 0 || 8 * rem >= 7 * slots || slices < 2 * kShortRun) return sp;
   sp.dp_tiles = total - rem;
   const int64_t work = rem * slices;
-  sp.workers = std::min<int64_t>(slots, std::max<int64_t>(1, work / kMinSlices));
+  const int64_t cap = std::max(cus * std::min<int64_t>(per_cu, 2), rem);
+  const int64_t want = std::max(work / kLongRun, std::min(cus, work / kShortRun));
+  sp.workers = std::min(cap, std::max<int64_t>(1, want));
   sp.base = work / sp.workers;
   sp.extra = work % sp.workers;
-  // The kernels handle runs of at most one tile (two pieces): rem < slots
-  // gives base < slices when workers == slots, and base < 2 * kMinSlices <=
-  // slices otherwise.
+  // The kernels handle runs of at most one tile (two pieces). Both cap and
+  // want are at least rem (slices >= kLongRun), so base <= slices, with
+  // extra == 0 if equal.
   if (sp.base + (sp.extra > 0 ? 1 : 0) > slices) hp::fail(HP_E_HIP, "internal: stream-K run longer than a tile");
   return sp;
 }
@@ -1065,7 +1077,7 @@ void launch_split(hp_ctx* ctx, Whole whole, Cut cut, Fix fixup, int threads, con
                   int64_t m, int64_t n, int64_t k, const BatchDesc& bd, const TileMap& tm, int64_t bk,
                   const char* name, bool moved) {
   const int per_cu = std::min(resident_per_cu(whole, threads), resident_per_cu(cut, threads));
-  Split sp = plan_split(tm.total, hp::ceil_div(k, bk), int64_t(ctx->compute_units) * per_cu);
+  Split sp = plan_split(tm.total, hp::ceil_div(k, bk), ctx->compute_units, per_cu);
   sp.moved = moved;
   if (sp.dp_tiles > 0) {
     whole<<<sp.dp_tiles, threads, 0, ctx->stream>>>(a, b, c, m, n, k, bd, tm, sp);

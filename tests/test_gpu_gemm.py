@@ -141,7 +141,7 @@ def test_kernel_modes_against_float64(hip, dtype, m, n, k):
 STREAM_K_CASES = [
     (np.float32, (), 512, 256, 8192),  # 256 x 256 tiles: interior, 2 tiles x 512 slices
     (np.float32, (), 1000, 700, 4100),  # 256 x 256 tiles: edges, K % 16 == 4
-    (np.float32, (2,), 600, 300, 4096),  # 256 x 256 tiles: batched, moved edge tiles
+    (np.float32, (2,), 600, 300, 4112),  # 256 x 256 tiles: batched, moved edge tiles
     (np.float32, (), 512, 256, 1552),  # interior, 2 tiles x 97 slices
     (np.float32, (), 31, 33, 4099),  # one tile cut over 32 workers
     (np.float32, (), 1000, 700, 2000),  # M/N edges, 12 tiles
@@ -149,7 +149,7 @@ STREAM_K_CASES = [
     (np.float32, (3,), 300, 200, 700),  # batched: 6 tiles
     (np.float32, (2,), 600, 300, 512),  # batched, moved edge tiles summed by the fixup
     (np.float32, (), 257, 257, 4096),  # single-row/column moved tiles cut over many workers
-    (np.float64, (), 1000, 1000, 2000),  # 32 tiles over 256 workers, extra > 0
+    (np.float64, (), 1000, 1000, 2100),  # 32 tiles over 256 workers, extra > 0
     (np.float64, (2,), 256, 384, 1024),  # interior fp64, batched
     (np.float64, (), 129, 65, 3001),  # K odd, fp64
 ]
