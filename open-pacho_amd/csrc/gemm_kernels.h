@@ -725,6 +725,179 @@ __global__ __launch_bounds__(CFG::kThreads, CFG::kMinBlocks) void kernel(const f
 
 }  // namespace f32
 
+// ---------------------------------------------------------- fp32 narrow ----
+
+// 64 x 64 output tiles, one workgroup each, for products whose 256 x 256 and
+// 128 x 128 tiles leave compute units idle or need stream-K (1024^3: 16 and
+// 64 tiles, against 256 here). Each of the workgroup's KW waves computes the
+// whole tile (4 x 4 MFMA blocks) over every KW-th K slice, from LDS buffers
+// of its own: no barrier in the K loop, no partial tiles in global memory and
+// no second kernel. At the end the KW accumulator tiles are added in wave
+// order through LDS, so results are deterministic. Interior products only:
+// M and N multiples of 64, K of 16, operand rows 16-byte aligned.
+namespace narrow {
+
+constexpr int T = 64;
+// LDS per slice and operand. A k-contiguous operand keeps rows of 16 k in
+// swizzled quads (fragment reads as in the tiled kernel). A K-strided one
+// ([k][rows] in memory) arrives as 4 k rows (1 KB) per LDS-DMA; 16 floats of
+// padding between those groups put the four lane groups of a fragment read
+// (k = 4 g + q) on disjoint banks (272 = 16 mod 64).
+constexpr int kGroup = 4 * T + 16;
+constexpr int kOperand = 4 * kGroup;  // >= T * 16, the k-contiguous size
+constexpr int kSlice = 2 * kOperand;  // A then B
+
+template <bool KM>
+struct Operand {
+  // Issue the LDS-DMA of one slice (16 k from k0) of a 64-row operand whose
+  // tile origin is p: KM = false, element (r, k) at p[r * ld + k]; KM = true,
+  // at p[k * ld + r]. Four 1 KB transfers per wave, all in bounds.
+  __device__ __forceinline__ static void issue(const float* p, int64_t ld, int64_t k0, float* buf, int lane) {
+#pragma unroll
+    for (int c = 0; c < 4; ++c) {
+      const float* src;
+      float* dst;
+      if constexpr (KM) {
+        src = p + (k0 + 4 * c + (lane >> 4)) * ld + 4 * (lane & 15);
+        dst = buf + c * kGroup;
+      } else {
+        const int row = 16 * c + (lane >> 2);
+        src = p + row * ld + k0 + 4 * ((lane & 3) ^ f32::swizzle(row));
+        dst = buf + 256 * c;
+      }
+      __builtin_amdgcn_global_load_lds(static_cast<const void*>(src),
+                                       (__attribute__((address_space(3))) void*)dst, 16, 0, 0);
+    }
+  }
+  // Fragment f (tile rows 16 f + lane % 16): k = 4 (lane / 16) + q in
+  // element q, the k order of the tiled kernel's fragments.
+  __device__ __forceinline__ static hpd::f32x4 frag(const float* buf, int f, int lane) {
+    if constexpr (KM) {
+      const float* base = buf + (lane >> 4) * kGroup + 16 * f + (lane & 15);
+      return hpd::f32x4{base[0], base[T], base[2 * T], base[3 * T]};
+    } else {
+      const int row = 16 * f + (lane & 15);
+      return *reinterpret_cast<const hpd::f32x4*>(buf + row * 16 + 4 * ((lane >> 4) ^ f32::swizzle(row)));
+    }
+  }
+};
+
+// s_waitcnt vmcnt(n), other counters at their maxima.
+template <int N>
+__device__ __forceinline__ void wait_vm() {
+  static_assert(N >= 0 && N < 16, "vmcnt immediate");
+  __builtin_amdgcn_s_waitcnt(kWaitVmcnt0 | N);
+}
+
+template <bool TA, bool TB, int KW>
+__global__ __launch_bounds__(64 * KW) void kernel(const float* __restrict__ A, const float* __restrict__ B,
+                                                  float* __restrict__ C, int64_t M, int64_t N, int64_t K,
+                                                  BatchDesc bd, TileMap tmap) {
+  // Buffer 0 and 1 of every wave: [KW][A slice, B slice].
+  __shared__ __attribute__((aligned(16))) float L0[KW * kSlice];
+  __shared__ __attribute__((aligned(16))) float L1[KW * kSlice];
+  using OA = Operand<TA>;   // A is K-strided when transposed
+  using OB = Operand<!TB>;  // B is K-strided unless transposed
+  const int lane = threadIdx.x & 63;
+  const int wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
+
+  const int64_t tile = xcd_major(blockIdx.x, tmap.total);
+  int64_t batch, ti, tj;
+  logical_tile(tile, tmap, batch, ti, tj);
+  int64_t a_off, b_off;
+  batch_offsets(batch, bd, a_off, b_off);
+  const int64_t m0 = ti * T, n0 = tj * T;
+  const float* Ap = A + a_off + (TA ? m0 : m0 * tmap.lda);
+  const float* Bp = B + b_off + (TB ? n0 * tmap.ldb : n0);
+
+  // This wave's slices: wave, wave + KW, ...
+  const int64_t slices = K / 16;
+  const int64_t count = slices > wave ? (slices - wave + KW - 1) / KW : 0;
+  float* const b0 = L0 + wave * kSlice;
+  float* const b1 = L1 + wave * kSlice;
+  auto issue = [&](int64_t t, float* buf) {
+    const int64_t k0 = (wave + t * KW) * 16;
+    OA::issue(Ap, tmap.lda, k0, buf, lane);
+    OB::issue(Bp, tmap.ldb, k0, buf + kOperand, lane);
+  };
+
+  hpd::f32x4 acc[4][4];
+#pragma unroll
+  for (int i = 0; i < 4; ++i)
+#pragma unroll
+    for (int j = 0; j < 4; ++j) acc[i][j] = hpd::f32x4{0.f, 0.f, 0.f, 0.f};
+  // Fragments of the current slice and of the next one; the two sets swap
+  // roles every slice (the loop body covers two).
+  hpd::f32x4 a0[4], b0f[4], a1[4], b1f[4];
+  auto read = [&](const float* buf, hpd::f32x4* fa, hpd::f32x4* fb) {
+#pragma unroll
+    for (int i = 0; i < 4; ++i) {
+      fa[i] = OA::frag(buf, i, lane);
+      fb[i] = OB::frag(buf + kOperand, i, lane);
+    }
+  };
+
+  if (count > 0) issue(0, b0);
+  if (count > 1) issue(1, b1);
+  wait_vm<0>();
+  read(b0, a0, b0f);
+  // Slice t (fragments in fa, fb): once every LDS-DMA has landed (only slice
+  // t + 1's can be in flight), read slice t + 1 into na, nb, then issue slice
+  // t + 2's LDS-DMA into `cur` (slice t was read from it: lgkmcnt(0)), then
+  // the MFMAs. No LDS read follows an LDS-DMA still in flight, so none waits
+  // for one. Reads past the last slice return stale LDS and go unused; they
+  // are unconditional so that the fragments stay in fixed registers.
+  auto slice = [&](int64_t t, float* cur, const float* nxt, const hpd::f32x4* fa, const hpd::f32x4* fb,
+                   hpd::f32x4* na, hpd::f32x4* nb) {
+    __builtin_amdgcn_s_waitcnt(0xC07F);  // lgkmcnt(0)
+    wait_vm<0>();
+    read(nxt, na, nb);
+    if (t + 2 < count) issue(t + 2, cur);
+#pragma unroll
+    for (int i = 0; i < 4; ++i)
+#pragma unroll
+      for (int q = 0; q < 4; ++q)
+#pragma unroll
+        for (int j = 0; j < 4; ++j)
+          acc[i][j] = __builtin_amdgcn_mfma_f32_16x16x4f32(fa[i][q], fb[j][q], acc[i][j], 0, 0, 0);
+  };
+  int64_t t = 0;
+  for (; t + 1 < count; t += 2) {
+    slice(t, b0, b1, a0, b0f, a1, b1f);
+    slice(t + 1, b1, b0, a1, b1f, a0, b0f);
+  }
+  if (t < count) slice(t, b0, b1, a0, b0f, a1, b1f);
+
+  // Sum the KW accumulator tiles in wave order: waves [0, KW/2) stage theirs
+  // in L0, the rest in L1 (16 KB each), then every thread adds whole
+  // accumulator groups and stores them.
+  __syncthreads();
+  constexpr int kHalf = KW / 2 > 0 ? KW / 2 : 1;
+  static_assert(kHalf * 16 * 64 * 4 <= KW * kSlice, "accumulators fit the slice buffers");
+  auto stage = [&](int w) -> hpd::f32x4* {
+    return reinterpret_cast<hpd::f32x4*>(w < kHalf ? L0 : L1) + (w % kHalf) * 16 * 64;
+  };
+  hpd::f32x4* mine = stage(wave);
+#pragma unroll
+  for (int i = 0; i < 4; ++i)
+#pragma unroll
+    for (int j = 0; j < 4; ++j) mine[(i * 4 + j) * 64 + lane] = acc[i][j];
+  __syncthreads();
+  float* Cb = C + batch * M * tmap.ldc;
+  for (int e = threadIdx.x; e < 16 * 64; e += 64 * KW) {
+    hpd::f32x4 sum = stage(0)[e];
+#pragma unroll
+    for (int w = 1; w < KW; ++w) sum += stage(w)[e];
+    const int blk = e >> 6, l = e & 63;
+    const int i = blk >> 2, j = blk & 3;
+    const int64_t col = n0 + 16 * j + (l & 15);
+#pragma unroll
+    for (int r = 0; r < 4; ++r) Cb[(m0 + 16 * i + 4 * (l >> 4) + r) * tmap.ldc + col] = sum[r];
+  }
+}
+
+}  // namespace narrow
+
 // ------------------------------------------------------------------ fp64 ----
 
 namespace f64 {
@@ -1061,11 +1234,17 @@ Split plan_split(int64_t total, int64_t slices, int64_t cus, int64_t per_cu) {
   const int64_t cap = std::max(cus * std::min<int64_t>(per_cu, 2), rem);
   const int64_t want = std::max(work / kLongRun, std::min(cus, work / kShortRun));
   sp.workers = std::min(cap, std::max<int64_t>(1, want));
+  // One worker per cut tile runs whole tiles: no pieces, no fixup.
+  if (sp.workers == rem) {
+    sp.dp_tiles = total;
+    sp.workers = 0;
+    return sp;
+  }
   sp.base = work / sp.workers;
   sp.extra = work % sp.workers;
   // The kernels handle runs of at most one tile (two pieces). Both cap and
-  // want are at least rem (slices >= kLongRun), so base <= slices, with
-  // extra == 0 if equal.
+  // want are at least rem (slices >= kLongRun), and workers > rem here, so
+  // base < slices.
   if (sp.base + (sp.extra > 0 ? 1 : 0) > slices) hp::fail(HP_E_HIP, "internal: stream-K run longer than a tile");
   return sp;
 }
@@ -1170,22 +1349,69 @@ void run_f32_config(hp_ctx* ctx, const float* a, const float* b, float* c, int64
 // unit but moves twice the operand bytes per flop, so it loses where Big
 // runs whole rounds (4096 x 4096 x 1024: 114 against 133 TFLOP/s) and where
 // stream-K runs are long. Measured on one MI355X, TFLOP/s Big / Small:
-//   1024^3 42 / 62, 1536^3 85 / 90, 1024 x 1024 x 4096 94 / 97,
-//   64 x (512 x 1024 @ 1024 x 768) 124 / 128, 6144 x 4096 x 1024 124 / 128;
-//   1024 x 1024 x 16384 124 / 121, 6144 x 4096 x 2048 132 / 131,
-//   4097 x 3001 x 2049 113 / 109, 8192 x 1024 x 4096 130 / 124.
+//   1536^3 86 / 94, 1024 x 1024 x 4096 96 / 105, 2048^3 113 / 116,
+//   64 x (512 x 1024 @ 1024 x 768) 126 / 128, 6144 x 4096 x 1024 126 / 128;
+//   2048 x 2048 x 4096 127 / 124, 3072^2 x 1024 110 / 92,
+//   4097 x 3001 x 2049 116 / 111, 8192 x 1024 x 4096 134 / 130.
 inline bool small_tiles(hp_ctx* ctx, int64_t m, int64_t n, int64_t k, int64_t batch) {
   using f32::Big;
+  using f32::Small;
   const int64_t tiles = hp::ceil_div(m, Big::BM) * hp::ceil_div(n, Big::BN) * batch;
   const int64_t cus = ctx->compute_units, slices = hp::ceil_div(k, f32::BK);
   if (tiles >= 2 * cus || tiles % cus == 0) return false;
+  // Small runs three workgroups per compute unit; a partly filled round of
+  // more than two per compute unit runs whole tiles unevenly (3072^2 x 1024:
+  // 95 against Big's 110 TFLOP/s).
+  const int64_t small = hp::ceil_div(m, Small::BM) * hp::ceil_div(n, Small::BN) * batch;
+  if (small > 2 * cus && small % (3 * cus) != 0) return false;
   return slices <= 64 || (4 * tiles <= cus && slices <= 256);
+}
+
+// The narrow kernel's interior contract: M and N multiples of 64, K of 16,
+// every operand row 16-byte aligned (LDS-DMA of both operands).
+template <bool TA, bool TB>
+bool narrow_fits(const float* a, const float* b, const BatchDesc& bd, int64_t m, int64_t n, int64_t k, int64_t lda,
+                 int64_t ldb) {
+  return m % narrow::T == 0 && n % narrow::T == 0 && k % 16 == 0 && k > 0 && lda % 4 == 0 && ldb % 4 == 0 &&
+         dma_aligned<float, TA, TB>(a, b, bd) && rows_aligned<TA, TB>(a, b, bd, m, n, lda, ldb);
+}
+
+// Narrow tiles for short products that the 64 x 64 tiles spread over the
+// chip: one to four tiles per compute unit and at most 2^23 multiply-adds
+// per compute unit. There the narrow kernel's missing stream-K and fixup
+// launch outweigh its lower MFMA rate; on longer products the 256 x 256 and
+// 128 x 128 kernels win. Measured on one MI355X, TFLOP/s narrow / otherwise:
+//   1024^3 90 / 67, 1024 x 1024 x 2048 97 / 86, 2048 x 2048 x 512 90 / 82;
+//   1024 x 1024 x 4096 105 / 105, 2048 x 2048 x 1024 101 / 103,
+//   1536^3 78 / 95, 512 x 512 x 8192 27 / 55, 8 x 1024^3 106 / 119.
+// Four waves per tile (two workgroups per compute unit) beat eight (one) on
+// every one of these shapes.
+constexpr int kNarrowWaves = 4;
+
+inline bool narrow_tiles(hp_ctx* ctx, int64_t m, int64_t n, int64_t k, int64_t batch) {
+  const int64_t cus = ctx->compute_units;
+  const int64_t tiles = hp::ceil_div(m, narrow::T) * hp::ceil_div(n, narrow::T) * batch;
+  if (tiles < cus || tiles > 4 * cus) return false;
+  // m n k batch <= 2^23 cus, without overflow (each factor < 2^31 here).
+  const double work = double(m) * double(n) * double(k) * double(batch);
+  return work <= double(cus) * double(int64_t(1) << 23);
+}
+
+template <bool TA, bool TB>
+void run_f32_narrow(hp_ctx* ctx, const float* a, const float* b, float* c, int64_t m, int64_t n, int64_t k,
+                    const BatchDesc& bd, int64_t batch, int64_t lda, int64_t ldb, int64_t ldc) {
+  TileMap tm;
+  prepare(m, n, batch, narrow::T, narrow::T, tm, lda, ldb, ldc);
+  narrow::kernel<TA, TB, kNarrowWaves><<<tm.total, 64 * kNarrowWaves, 0, ctx->stream>>>(a, b, c, m, n, k, bd, tm);
+  hp::check_launch("gemm_f32");
 }
 
 template <bool TA, bool TB>
 void run_f32_tiles(hp_ctx* ctx, const float* a, const float* b, float* c, int64_t m, int64_t n, int64_t k,
                    const BatchDesc& bd, int64_t batch, int64_t lda, int64_t ldb, int64_t ldc) {
-  if (small_tiles(ctx, m, n, k, batch)) {
+  if (narrow_tiles(ctx, m, n, k, batch) && narrow_fits<TA, TB>(a, b, bd, m, n, k, lda, ldb)) {
+    run_f32_narrow<TA, TB>(ctx, a, b, c, m, n, k, bd, batch, lda, ldb, ldc);
+  } else if (small_tiles(ctx, m, n, k, batch)) {
     run_f32_config<f32::Small, TA, TB>(ctx, a, b, c, m, n, k, bd, batch, lda, ldb, ldc);
   } else {
     run_f32_config<f32::Big, TA, TB>(ctx, a, b, c, m, n, k, bd, batch, lda, ldb, ldc);

@@ -72,9 +72,11 @@ def test_streaming_kernels_do_not_spill(resources, unit):
 #    first uses them), a late wave can read slice 2's data (seen as one wrong
 #    16 x 64 fragment block in batched products with several workgroups per
 #    compute unit).
-# 2. No fragment read waits for vmcnt: the LDS-DMA in flight during a slice
-#    writes the other buffer. A wait there (the compiler adds one for some
-#    placements of that barrier) cost 8192^3 4% of peak.
+# 2. No fragment read of the tiled kernels waits for vmcnt: the LDS-DMA in
+#    flight during a slice writes the other buffer. A wait there (the
+#    compiler adds one for some placements of that barrier) cost 8192^3 4% of
+#    peak. (The narrow kernel waits for its DMA by design at the start of
+#    each slice, before it reads the next slice; it has no such barrier.)
 @pytest.mark.parametrize("unit", [f"gemm_{t}_{layout}" for t in ("f32", "f64") for layout in ("nn", "nt", "tn", "tt")])
 def test_gemm_lds_reads_keep_their_barriers_and_skip_dma_waits(unit, tmp_path):
     import importlib.util
@@ -103,11 +105,11 @@ def test_gemm_lds_reads_keep_their_barriers_and_skip_dma_waits(unit, tmp_path):
             barriers[kernel].append(0)
         elif text.startswith("ds_read") and barriers[kernel]:
             barriers[kernel][-1] += 1  # LDS reads after the latest barrier
-        if text.startswith("ds_read"):
+        if text.startswith("ds_read") and "narrow" not in kernel:
             assert not previous.startswith("s_waitcnt vmcnt"), f"fragment read waits for vmcnt in {kernel}"
         previous = text
     for kernel, reads in barriers.items():
-        if "kernel" in kernel and len(reads) >= 2:
+        if "kernel" in kernel and "narrow" not in kernel and len(reads) >= 2:
             checked.add(kernel)
             assert reads[0] > 0, f"no LDS reads between the first two barriers (sunk reads) in {kernel}"
     assert checked, unit

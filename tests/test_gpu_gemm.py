@@ -356,6 +356,48 @@ def test_padding_preserves_special_values_and_signed_zero(hip):
     np.testing.assert_array_equal(p.asnumpy(a), left)
 
 
+# ---- narrow 64 x 64 tiles: short products with M, N multiples of 64 and K
+# of 16 that give one to four such tiles per compute unit (256 to 1024 on
+# MI355X) and at most 2^23 multiply-adds per compute unit. Each tile is one
+# workgroup whose four waves take every fourth K slice and add their tiles
+# in wave order, so a wave may own one slice or none.
+
+NARROW_CASES = [
+    ((), 1024, 1024, 16),  # one slice: three waves own none
+    ((), 1024, 1024, 48),  # three slices: one wave owns none
+    ((), 1024, 1024, 1024),
+    ((), 2048, 512, 2048),  # long K: 32 slices per wave
+    ((), 1024, 2048, 80),  # two tiles per compute unit
+    ((), 2048, 2048, 512),  # four tiles per compute unit
+    ((4,), 512, 512, 144),  # batched
+]
+
+
+@pytest.mark.parametrize("ta,tb", [(False, False), (True, False), (False, True), (True, True)])
+@pytest.mark.parametrize("batch,m,n,k", NARROW_CASES)
+def test_narrow_tiles_against_float64_and_deterministic(hip, ta, tb, batch, m, n, k):
+    if batch and (ta or tb):
+        pytest.skip("transposed operands are 2-D")
+    rng = np.random.default_rng(m + 5 * n + 11 * k + 2 * ta + tb)
+    left = rng.uniform(-1, 1, batch + ((k, m) if ta else (m, k))).astype(np.float32)
+    right = rng.uniform(-1, 1, (n, k) if tb else (k, n)).astype(np.float32)
+    a, b = p.asarray(left, backend=hip), p.asarray(right, backend=hip)
+    product = p.compile(lambda x, y: (x.T if ta else x) @ (y.T if tb else y))
+    got = p.asnumpy(product(a, b))
+    np.testing.assert_array_equal(got, p.asnumpy(product(a, b)))  # fixed wave order: repeatable
+    op_a = (left.T if ta else left).astype(np.float64)
+    op_b = (right.T if tb else right).astype(np.float64)
+    want = op_a @ op_b
+    scale = np.abs(op_a) @ np.abs(op_b)
+    bound = 4e-7 * np.sqrt(k) * 4
+    assert np.all(np.abs(got - want) <= bound * scale + 1e-30)
+    if ta or tb:
+        # The materialized transposes give the same bits (same tiles, same K order).
+        eager = p.asnumpy(p.asarray(np.ascontiguousarray(op_a.astype(np.float32)), backend=hip)
+                          @ p.asarray(np.ascontiguousarray(op_b.astype(np.float32)), backend=hip))
+        np.testing.assert_array_equal(got, eager)
+
+
 # ---- products of private transposes (hp_gemm_layout), reference
 # tests/test_clblast.py:410-440 and tests/test_compiled_layout.py:43-80
 
