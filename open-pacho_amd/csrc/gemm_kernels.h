@@ -260,9 +260,57 @@ struct SliceLoader {
   __device__ __forceinline__ static int64_t origin(int64_t s0, int64_t ld) { return KM ? s0 * 16 * ld : s0 * 16; }
 };
 
+// LDS-DMA through a buffer resource: 16 bytes per lane from base + voffset +
+// soffset into LDS at `lds` (the wave's base; lane l lands at lds + 16 l).
+// The MUBUF form, unlike global_load_lds, is not taken by the compiler for
+// an access to both memory and LDS: after a global_load_lds it waits for
+// every pending LDS read (lgkmcnt(0)) at the next use of any of them, the
+// buffer form leaves its in-order lgkmcnt counts intact. Offsets are 32-bit:
+// hosts route operands whose tile spans reach 2^31 bytes elsewhere. Third
+// descriptor dword 0x00020000: 32-bit data format (gfx9).
+__device__ __forceinline__ __amdgpu_buffer_rsrc_t buffer_rsrc(const void* base) {
+  return __builtin_amdgcn_make_buffer_rsrc(const_cast<void*>(base), 0, 0x7FFFFFFF, 0x00020000);
+}
+__device__ __forceinline__ void dma16(__amdgpu_buffer_rsrc_t rsrc, void* lds, unsigned voffset, unsigned soffset) {
+  __builtin_amdgcn_raw_ptr_buffer_load_lds(rsrc, (__attribute__((address_space(3))) void*)lds, 16, voffset, soffset, 0,
+                                           0);
+}
+
 // s_waitcnt vmcnt(0) (gfx9 encoding: vmcnt in bits 3:0 and 15:14, expcnt
 // 6:4, lgkmcnt 11:8 left at their maxima).
 constexpr unsigned kWaitVmcnt0 = 0x0F70;
+
+// s_waitcnt vmcnt(N), the other counters at their maxima.
+template <int N>
+__device__ __forceinline__ void wait_vmcnt() {
+  static_assert(N >= 0 && N < 16, "vmcnt immediate");
+  __builtin_amdgcn_s_waitcnt(kWaitVmcnt0 | N);
+}
+
+// Workgroup barrier without any wait: neither the wave's LDS reads nor its
+// LDS-DMA (callers wait for what the barrier publishes themselves).
+__device__ __forceinline__ void dma_barrier() { __builtin_amdgcn_s_barrier(); }
+
+// Workgroup barrier for LDS that leaves LDS-DMA in flight: every LDS read
+// and write of this wave completes (lgkmcnt(0)), then s_barrier. A
+// __syncthreads() fence also waits for vmcnt(0), since the DMA writes LDS,
+// which would drain the loads of the slice after next. Callers wait for the
+// DMA that the barrier publishes themselves (wait_vmcnt). The loops that use
+// it keep every LDS access that must not cross it on its own side through
+// data dependences: fragment reads feed the next iteration's MFMAs, DMA
+// destinations rotate through buffers that the reads cannot prove distinct.
+__device__ __forceinline__ void lds_barrier() {
+  __builtin_amdgcn_s_waitcnt(0xC07F);  // lgkmcnt(0)
+  __builtin_amdgcn_s_barrier();
+}
+
+// LDS-DMA instructions per wave and slice of two direct loaders (0 when
+// either one is register-staged).
+template <class LA, class LB>
+constexpr int slice_loads() {
+  if constexpr (LA::kDirect && LB::kDirect) return LA::kLoads + LB::kLoads;
+  else return 0;
+}
 
 // ------------------------------------------------------------------ fp32 ----
 
@@ -390,20 +438,22 @@ struct DmaLoader {
     lane = tid & 63;
   }
 
-  __device__ __forceinline__ void issue(const float* p, int64_t r0, int64_t rows, int64_t ld, int64_t, int64_t k0,
+  // Element (r, k) of the tile at p[(r0 + r) * ld + k]; byte offsets from
+  // the tile's first row: ROWS * ld * 4 < 2^31 (host check).
+  __device__ __forceinline__ void issue(const float* p, int64_t r0, int64_t, int64_t ld, int64_t, int64_t k0,
                                         float* buf) const {
+    const __amdgpu_buffer_rsrc_t rsrc = buffer_rsrc(p + r0 * ld);
 #pragma unroll
     for (int i = 0; i < kChunks; ++i) {
       const int c = chunk0 + i;
-      const int row = 16 * c + (lane >> 2);
-      const float* src = p + (r0 + row) * ld + k0 + 4 * ((lane & 3) ^ swizzle(row));
-      // The LDS operand is an address-space-3 pointer: a C cast converts it.
-      __builtin_amdgcn_global_load_lds(static_cast<const void*>(src),
-                                       (__attribute__((address_space(3))) void*)(buf + 256 * c), 16, 0, 0);
+      const unsigned row = 16 * c + (lane >> 2);
+      const unsigned element = row * unsigned(ld) + 4 * ((lane & 3) ^ swizzle(row));
+      dma16(rsrc, buf + 256 * c, 4 * element, 4 * unsigned(k0));
     }
   }
   __device__ __forceinline__ void commit(float*) const {}
   static constexpr bool kDirect = true;
+  static constexpr int kLoads = kChunks;  // LDS-DMA instructions per wave and slice
 
   __device__ __forceinline__ static int64_t origin(int64_t s0, int64_t) { return s0 * 16; }
 };
@@ -441,18 +491,20 @@ struct RowDmaLoader {
     lane = tid & 63;
   }
 
+  // Element (r, k) at p[k * ld + r0 + r]; byte offsets from the tile's
+  // first column: (K * ld + ROWS) * 4 < 2^31 (host check).
   __device__ __forceinline__ void issue(const float* p, int64_t r0, int64_t, int64_t ld, int64_t, int64_t k0,
                                         float* buf) const {
+    const __amdgpu_buffer_rsrc_t rsrc = buffer_rsrc(p + r0);
 #pragma unroll
     for (int i = 0; i < kRowsPerWave; ++i) {
-      const int k = k0w + i;
-      const float* src = p + (k0 + k) * ld + r0 + 4 * lane;
-      __builtin_amdgcn_global_load_lds(static_cast<const void*>(src),
-                                       (__attribute__((address_space(3))) void*)(buf + k * RS), 16, 0, 0);
+      const unsigned k = k0w + i;
+      dma16(rsrc, buf + k * RS, 4 * (k * unsigned(ld) + 4 * lane), 4 * unsigned(k0 * ld));
     }
   }
   __device__ __forceinline__ void commit(float*) const {}
   static constexpr bool kDirect = true;
+  static constexpr int kLoads = kRowsPerWave;  // LDS-DMA instructions per wave and slice
 
   __device__ __forceinline__ static int64_t origin(int64_t s0, int64_t ld) { return s0 * 16 * ld; }
   // Fragment base of lane `lane` for tile rows row0 + (lane & 15).
@@ -537,11 +589,16 @@ __global__ __launch_bounds__(CFG::kThreads, CFG::kMinBlocks) void kernel(const f
   using LA = typename std::conditional<kRowA, RowDmaLoader<BM, kThreads>, Loader<TA, MODE, BM, kThreads>>::type;
   using LB = typename std::conditional<kRowB, RowDmaLoader<BN, kThreads>, Loader<!TB, MODE, BN, kThreads>>::type;
   constexpr int kBufA = buf_floats<LA, kRowA, BM * SA>(), kBufB = buf_floats<LB, kRowB, BN * SB>();
-  // Double-buffered slices, one LDS variable per buffer and operand.
+  // Slices in LDS, one variable per buffer and operand: three buffers when
+  // both operands arrive by LDS-DMA (loads run two slices ahead), else two.
+  constexpr int kStages = LA::kDirect && LB::kDirect ? 3 : 2;
+  constexpr int kSliceLoads = slice_loads<LA, LB>();
   __shared__ __attribute__((aligned(16))) float As0[kBufA];
   __shared__ __attribute__((aligned(16))) float As1[kBufA];
+  __shared__ __attribute__((aligned(16))) float As2[kStages == 3 ? kBufA : 4];
   __shared__ __attribute__((aligned(16))) float Bs0[kBufB];
   __shared__ __attribute__((aligned(16))) float Bs1[kBufB];
+  __shared__ __attribute__((aligned(16))) float Bs2[kStages == 3 ? kBufB : 4];
 
   const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
   const int wm = wave / CFG::WAVES_N, wn = wave % CFG::WAVES_N;
@@ -616,18 +673,26 @@ __global__ __launch_bounds__(CFG::kThreads, CFG::kMinBlocks) void kernel(const f
 #pragma unroll
       for (int j = 0; j < FN; ++j) acc[i][j] = hpd::f32x4{0.f, 0.f, 0.f, 0.f};
 
-    load_slice(0, As0, Bs0);
-    store_slice(As0, Bs0);
-    if (slices > 1) {
-      load_slice(BK, As1, Bs1);
-      store_slice(As1, Bs1);
+    if constexpr (kStages == 3) {
+      load_slice(0, As0, Bs0);
+      if (slices > 1) load_slice(BK, As1, Bs1);
+      publish();
+    } else {
+      load_slice(0, As0, Bs0);
+      store_slice(As0, Bs0);
+      if (slices > 1) {
+        load_slice(BK, As1, Bs1);
+        store_slice(As1, Bs1);
+      }
+      publish();
     }
-    publish();
     hpd::f32x4 a[FM], b[FN], b_next[FN];
-#pragma unroll
-    for (int i = 0; i < FM; ++i) a[i] = frag_a(As0 + a_read, i);
+    // B first: the loop's first MFMAs then wait on the same in-order LDS
+    // counts as after a slice of the loop, whose last reads are A's.
 #pragma unroll
     for (int j = 0; j < FN; ++j) b[j] = frag_b(Bs0 + b_read, j);
+#pragma unroll
+    for (int i = 0; i < FM; ++i) a[i] = frag_a(As0 + a_read, i);
     // Slice s: slice s+2 goes into the buffers (as, bs) that held slice s,
     // fragments of slice s+1 come from an, bn (buffer plus this lane's
     // fragment offset).
@@ -664,18 +729,82 @@ __global__ __launch_bounds__(CFG::kThreads, CFG::kMinBlocks) void kernel(const f
     // for vmcnt(0) before every fragment read of the loop (8192^3: -4% of
     // peak), and so did unrolling two slices per iteration over fixed
     // buffers (-2.5%). The assembly is checked for both in the CPU tests.
-    if (slices > 0) __syncthreads();
+    if (kStages == 2 && slices > 0) __syncthreads();
     // The next slice's fragment addresses are carried across iterations:
     // picking them per slice lets the compiler rematerialize the address
     // into each fragment register, and that write has to wait for the MFMAs
     // still reading the register (measured: -3% of peak).
     const float* an = As1 + a_read;
     const float* bn = Bs1 + b_read;
-    for (int64_t s = 0; s < slices; ++s) {
-      const bool odd = s & 1;
-      slice(s, odd ? As1 : As0, odd ? Bs1 : Bs0, an, bn);
-      an = (odd ? As1 : As0) + a_read;
-      bn = (odd ? Bs1 : Bs0) + b_read;
+    if constexpr (kStages == 3) {
+      // Slice s: slice s+2 goes into the third buffer (the one that held
+      // slice s-1), fragments of slice s+1 come from an, bn. Every wave read
+      // slice s-1's fragments before slice s-2's barrier and used them before
+      // slice s-1's, so the barrier that publishes a slice need not wait for
+      // the wave's own LDS reads: only the LDS-DMA it publishes. Refills are
+      // unconditional (past the last slice they read stale LDS and go unused)
+      // and the two B fragment sets swap roles every slice, so the next
+      // slice's first MFMAs wait only for reads issued early in this one.
+      auto slice3 = [&](int64_t s, float* as, float* bs, const float* an, const float* bn, hpd::f32x4* bc,
+                        hpd::f32x4* bx) {
+#pragma unroll
+        for (int i = 0; i < FM; ++i) {
+#pragma unroll
+          for (int q = 0; q < 4; ++q)
+#pragma unroll
+            for (int j = 0; j < FN; ++j)
+              acc[i][j] = __builtin_amdgcn_mfma_f32_16x16x4f32(a[i][q], bc[j][q], acc[i][j], 0, 0, 0);
+          // The compiler orders LDS reads and LDS-DMA with one counter and
+          // waits for every LDS read before the first fragment use after an
+          // LDS-DMA issue. Issued after fragment 0's MFMAs, with that
+          // fragment's refill held back to fragment 1, the DMA is followed by
+          // no read younger than the previous slice's last one.
+          if (i == 0) {
+            if (s + 2 < slices) load_slice((s + 2) * BK, as, bs);
+          } else {
+            if (i == 1) {
+              a[0] = frag_a(an, 0);
+              bx[0] = frag_b(bn, 0);
+            }
+            a[i] = frag_a(an, i);
+            if (i < FN) bx[i] = frag_b(bn, i);
+          }
+          // Keep the refills behind their fragment's MFMAs: without branches
+          // the scheduler otherwise interleaves the whole slice and renames
+          // accumulators.
+          __builtin_amdgcn_sched_barrier(0);
+        }
+        wait_vmcnt<0>();
+        dma_barrier();
+      };
+      float *a1 = As1, *a2 = As2, *a0 = As0, *b1 = Bs1, *b2 = Bs2, *b0 = Bs0;
+      auto rotate = [&] {
+        an = a2 + a_read;
+        bn = b2 + b_read;
+        float* t = a0;
+        a0 = a1;
+        a1 = a2;
+        a2 = t;
+        t = b0;
+        b0 = b1;
+        b1 = b2;
+        b2 = t;
+      };
+      int64_t s = 0;
+      for (; s + 1 < slices; s += 2) {
+        slice3(s, a2, b2, an, bn, b, b_next);
+        rotate();
+        slice3(s + 1, a2, b2, an, bn, b_next, b);
+        rotate();
+      }
+      if (s < slices) slice3(s, a2, b2, an, bn, b, b_next);
+    } else {
+      for (int64_t s = 0; s < slices; ++s) {
+        const bool odd = s & 1;
+        slice(s, odd ? As1 : As0, odd ? Bs1 : Bs0, an, bn);
+        an = (odd ? As1 : As0) + a_read;
+        bn = (odd ? Bs1 : Bs0) + b_read;
+      }
     }
 
     if (slot < 0) {
@@ -1296,6 +1425,18 @@ bool dma_aligned(const T* a, const T* b, const BatchDesc& bd) {
   return (TA || aligned(a, bd.a_stride)) && (!TB || aligned(b, bd.b_stride));
 }
 
+// The buffer-form LDS-DMA addresses an operand with 32-bit byte offsets
+// from its tile origin: a k-contiguous operand (A unless TA, B if TB) spans
+// rows * ld + k elements from there, a K-strided one k * ld + rows. Both
+// below 2^31 bytes, else the register-staged mode-2 loads serve the product.
+template <bool TA, bool TB>
+bool dma_offsets_fit(int64_t k, int64_t lda, int64_t ldb, int64_t bm, int64_t bn) {
+  auto fits = [](int64_t elements) { return elements < (int64_t(1) << 29); };
+  const int64_t a_span = TA ? k * lda + bm : bm * lda + k;
+  const int64_t b_span = TB ? bn * ldb + k : k * ldb + bn;
+  return fits(a_span) && fits(b_span);
+}
+
 // RowDmaLoader needs every k row of its operand (A if TA, B unless TB)
 // 16-byte aligned: the base pointer and each batch stride, the leading
 // dimension, and the tile origins along the rows (multiples of the tile, or
@@ -1324,7 +1465,7 @@ void run_f32_config(hp_ctx* ctx, const float* a, const float* b, float* c, int64
   prepare(m, n, batch, BM, BN, tm, lda, ldb, ldc);
   auto fix = fixup_kernel<float, hpd::f32x4, Layout<CFG>>;
   int mode = mode_of(m, n, k, BM, BN, BK);
-  if (!dma_aligned<float, TA, TB>(a, b, bd)) mode = 2;
+  if (!dma_aligned<float, TA, TB>(a, b, bd) || !dma_offsets_fit<TA, TB>(k, lda, ldb, BM, BN)) mode = 2;
   const bool rows = kRows && mode != 2 && rows_aligned<TA, TB>(a, b, bd, m, n, lda, ldb);
   auto run = [&](auto whole, auto cut, bool moved) {
     launch_split<float, BM, BN>(ctx, whole, cut, fix, T, a, b, c, m, n, k, bd, tm, BK, "gemm_f32", moved);
