@@ -691,8 +691,10 @@ __global__ __launch_bounds__(CFG::kThreads, CFG::kMinBlocks) void kernel(const f
     // counts as after a slice of the loop, whose last reads are A's.
 #pragma unroll
     for (int j = 0; j < FN; ++j) b[j] = frag_b(Bs0 + b_read, j);
+    __builtin_amdgcn_sched_barrier(0);
 #pragma unroll
     for (int i = 0; i < FM; ++i) a[i] = frag_a(As0 + a_read, i);
+    __builtin_amdgcn_sched_barrier(0);
     // Slice s: slice s+2 goes into the buffers (as, bs) that held slice s,
     // fragments of slice s+1 come from an, bn (buffer plus this lane's
     // fragment offset).
@@ -1056,16 +1058,17 @@ struct Layout {
 };
 
 // A k-contiguous fp64 operand in modes 0 and 1 (rows 16-byte aligned, host
-// check): its K slice goes from global memory straight into LDS with
-// global_load_lds_dwordx4, as in the fp32 kernel. One instruction fills a
-// 1 KB chunk of 8 rows; lane l writes row 8c + l / 8 at slot l % 8, so it
-// fetches the k pair that the swizzle stores there: (l % 8) ^ swizzle(row).
-// Rows past `rows` read clamped addresses (mode 1; outputs never stored).
+// check): its K slice goes from global memory straight into LDS by LDS-DMA
+// (dma16), as in the fp32 kernel. One instruction fills a 1 KB chunk of 8
+// rows; lane l writes row 8c + l / 8 at slot l % 8, so it fetches the k pair
+// that the swizzle stores there: (l % 8) ^ swizzle(row). Rows past `rows`
+// read clamped addresses (mode 1; outputs never stored).
 template <int ROWS, int MODE>
 struct DmaLoader64 {
   static_assert(MODE != 2, "the K-edge slice needs zero fill: staged loads only");
   static_assert(kThreads == 512 && ROWS % 64 == 0, "ROWS / 64 chunks of 8 rows per wave");
   static constexpr int kChunks = ROWS / 64;  // per wave
+  static constexpr int kLoads = kChunks;     // LDS-DMA instructions per wave and slice
   int chunk0, lane;
 
   __device__ __forceinline__ void init(int tid) {
@@ -1073,22 +1076,63 @@ struct DmaLoader64 {
     lane = tid & 63;
   }
 
+  // Byte offsets from the tile's first row: ROWS * ld * 8 < 2^31 (host check).
   __device__ __forceinline__ void issue(const double* p, int64_t r0, int64_t rows, int64_t ld, int64_t, int64_t k0,
                                         double* buf) const {
+    const __amdgpu_buffer_rsrc_t rsrc = buffer_rsrc(p + r0 * ld);
 #pragma unroll
     for (int i = 0; i < kChunks; ++i) {
       const int c = chunk0 + i;
-      const int row = 8 * c + (lane >> 3);
-      const int64_t r = MODE == 0 || r0 + row < rows ? r0 + row : rows - 1;
-      const double* src = p + r * ld + k0 + 2 * ((lane & 7) ^ swizzle(row));
-      // The LDS operand is an address-space-3 pointer: a C cast converts it.
-      __builtin_amdgcn_global_load_lds(static_cast<const void*>(src),
-                                       (__attribute__((address_space(3))) void*)(buf + 128 * c), 16, 0, 0);
+      const unsigned row = 8 * c + (lane >> 3);
+      const unsigned r = MODE == 0 || r0 + row < rows ? row : unsigned(rows - 1 - r0);
+      const unsigned element = r * unsigned(ld) + 2 * ((lane & 7) ^ swizzle(row));
+      dma16(rsrc, buf + 128 * c, 8 * element, 8 * unsigned(k0));
     }
   }
   __device__ __forceinline__ void commit(double*) const {}
   static constexpr bool kDirect = true;
   __device__ __forceinline__ static int64_t origin(int64_t s0, int64_t) { return s0 * 16; }
+};
+
+// A K-strided fp64 operand ([k][rows] in memory: B, or A transposed) in
+// modes 0 and 1, k rows 16-byte aligned (host check): each k row of the tile
+// (ROWS doubles, 1 KB per LDS-DMA) lands in LDS as [k][row] at a row stride
+// of RS doubles. A fragment (k pair 8h + 2g + {0, 1}, row r) is two 8-byte
+// reads RS apart, one ds_read2_b64 for 128-wide tiles. The 8-double pad
+// puts lane groups g and g + 1 (one 32-lane serving group) 128 bytes apart
+// in the banks, for both reads. Columns past the operand's end (mode 1 edge
+// tiles) read as 0 through the descriptor's range check; columns past `rows`
+// inside it feed outputs that are never stored.
+template <int ROWS>
+struct RowDma64 {
+  static constexpr int kPerRow = ROWS * 8 / 1024;  // LDS-DMA instructions per k row
+  static constexpr int kLoads = 16 * kPerRow / (kThreads / 64);
+  static_assert(kLoads * (kThreads / 64) == 16 * kPerRow, "whole k rows per wave");
+  static constexpr int RS = ROWS + 8;
+  static constexpr int kBufDoubles = 16 * RS;
+  int first, lane;
+
+  __device__ __forceinline__ void init(int tid) {
+    first = kLoads * __builtin_amdgcn_readfirstlane(tid >> 6);
+    lane = tid & 63;
+  }
+
+  // Element (r, k) at p[k * ld + r0 + r]; `extent` elements from p + r0 are
+  // in bounds. Byte offsets: (K * ld + ROWS) * 8 < 2^31 (host check).
+  __device__ __forceinline__ void issue(const double* p, int64_t r0, int64_t extent, int64_t ld, int64_t,
+                                        int64_t k0, double* buf) const {
+    const __amdgpu_buffer_rsrc_t rsrc =
+        __builtin_amdgcn_make_buffer_rsrc(const_cast<double*>(p + r0), 0, int(8 * extent), 0x00020000);
+#pragma unroll
+    for (int i = 0; i < kLoads; ++i) {
+      const unsigned t = first + i;
+      const unsigned k = t / kPerRow, c = t % kPerRow;
+      dma16(rsrc, buf + k * RS + 128 * c, 8 * (k * unsigned(ld) + 128 * c + 2 * lane), 8 * unsigned(k0 * ld));
+    }
+  }
+  __device__ __forceinline__ void commit(double*) const {}
+  static constexpr bool kDirect = true;
+  __device__ __forceinline__ static int64_t origin(int64_t s0, int64_t ld) { return s0 * 16 * ld; }
 };
 
 // Register-staged fp64 operand slices behind the same issue/commit interface.
@@ -1112,15 +1156,24 @@ using Loader = typename std::conditional<!KM && MODE != 2, DmaLoader64<ROWS, MOD
 // one barrier. A lane of MFMA lane group g = lane/16 reads the k pair
 // {2g, 2g+1} (half 0) or {8+2g, 9+2g} (half 1) with one ds_read_b128 and
 // feeds it to two MFMAs (k-permutation shared by A and B).
-template <int MODE, bool STREAM_K, bool TA, bool TB>
+template <int MODE, bool STREAM_K, bool TA, bool TB, bool ROWDMA>
 __global__ __launch_bounds__(kThreads, 1) void kernel(const double* __restrict__ A, const double* __restrict__ B,
                                                       double* __restrict__ C, int64_t M, int64_t N, int64_t K,
                                                       BatchDesc bd, TileMap tmap, Split sp) {
-  // Double-buffered slices, one LDS variable per buffer and operand.
-  __shared__ __attribute__((aligned(16))) double As0[BM * S];
-  __shared__ __attribute__((aligned(16))) double As1[BM * S];
-  __shared__ __attribute__((aligned(16))) double Bs0[BN * S];
-  __shared__ __attribute__((aligned(16))) double Bs1[BN * S];
+  // ROWDMA: K-strided operands (A if TA, B unless TB) arrive by RowDma64.
+  constexpr bool kRowA = TA && ROWDMA && MODE != 2, kRowB = !TB && ROWDMA && MODE != 2;
+  using LA = typename std::conditional<kRowA, RowDma64<BM>, Loader<BM, TA, MODE>>::type;
+  using LB = typename std::conditional<kRowB, RowDma64<BN>, Loader<BN, !TB, MODE>>::type;
+  constexpr int kBufA = kRowA ? RowDma64<BM>::kBufDoubles : BM * S;
+  constexpr int kBufB = kRowB ? RowDma64<BN>::kBufDoubles : BN * S;
+  // Three LDS stages when both operands arrive by LDS-DMA, else two.
+  constexpr int kStages = LA::kDirect && LB::kDirect ? 3 : 2;
+  __shared__ __attribute__((aligned(16))) double As0[kBufA];
+  __shared__ __attribute__((aligned(16))) double As1[kBufA];
+  __shared__ __attribute__((aligned(16))) double As2[kStages == 3 ? kBufA : 2];
+  __shared__ __attribute__((aligned(16))) double Bs0[kBufB];
+  __shared__ __attribute__((aligned(16))) double Bs1[kBufB];
+  __shared__ __attribute__((aligned(16))) double Bs2[kStages == 3 ? kBufB : 2];
 
   const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
   const int wm = wave >> 1, wn = wave & 1;
@@ -1131,18 +1184,33 @@ __global__ __launch_bounds__(kThreads, 1) void kernel(const double* __restrict__
   // contiguous bytes of one B row), stored as 2 pairs.
   // Edge tiles stay at their own origin and load clamped rows (modes 1, 2):
   // moving them inside, as the fp32 kernel does, measured no faster here.
-  Loader<BM, TA, MODE> la;
-  Loader<BN, !TB, MODE> lb;
+  LA la;
+  LB lb;
   constexpr bool kDirect = decltype(la)::kDirect || decltype(lb)::kDirect;
   la.init(tid);
   lb.init(tid);
   const int64_t lda = tmap.lda, ldb = tmap.ldb;
   // Fragment rows differ from (lane & 15) by multiples of 16: same swizzle.
   const int sw = swizzle(lane & 15), g = lane >> 4;
-  const int a_read0 = (wm * WM + (lane & 15)) * S + 2 * (g ^ sw);
-  const int a_read1 = (wm * WM + (lane & 15)) * S + 2 * ((4 + g) ^ sw);
-  const int b_read0 = (wn * WN + (lane & 15)) * S + 2 * (g ^ sw);
-  const int b_read1 = (wn * WN + (lane & 15)) * S + 2 * ((4 + g) ^ sw);
+  // Fragment offsets per k half: swizzled k-contiguous rows, or for a row-DMA
+  // operand ([k][row], stride RS) row 8h + 2g of the tile column.
+  auto read_offset = [&](bool rowdma, int rs, int row0, int h) {
+    return rowdma ? (8 * h + 2 * g) * rs + row0 + (lane & 15) : (row0 + (lane & 15)) * S + 2 * ((4 * h + g) ^ sw);
+  };
+  constexpr int kRsA = kRowA ? RowDma64<BM>::RS : S, kRsB = kRowB ? RowDma64<BN>::RS : S;
+  const int a_read0 = read_offset(kRowA, kRsA, wm * WM, 0), a_read1 = read_offset(kRowA, kRsA, wm * WM, 1);
+  const int b_read0 = read_offset(kRowB, kRsB, wn * WN, 0), b_read1 = read_offset(kRowB, kRsB, wn * WN, 1);
+  // Fragment f of half h: a k pair of tile rows 16 f + lane % 16.
+  auto frag_a = [&](const double* buf, int h, int f) {
+    const double* q = buf + (h ? a_read1 : a_read0);
+    if constexpr (kRowA) return hpd::f64x2{q[16 * f], q[16 * f + kRsA]};
+    else return *reinterpret_cast<const hpd::f64x2*>(q + 16 * f * S);
+  };
+  auto frag_b = [&](const double* buf, int h, int f) {
+    const double* q = buf + (h ? b_read1 : b_read0);
+    if constexpr (kRowB) return hpd::f64x2{q[16 * f], q[16 * f + kRsB]};
+    else return *reinterpret_cast<const hpd::f64x2*>(q + 16 * f * S);
+  };
 
   auto piece = [&](int64_t tile, int64_t s0, int64_t s1, int64_t slot) {
     int64_t batch, ti, tj;
@@ -1159,8 +1227,12 @@ __global__ __launch_bounds__(kThreads, 1) void kernel(const double* __restrict__
     // all-staged mode-2 kernels, one more inlined wrapper level reshuffled
     // registers into spills (transposed A: 23 -> 209 spilled VGPRs).
     auto load_slice = [&](int64_t k0, double* as, double* bs) {
-      if constexpr (decltype(la)::kDirect) la.issue(Ap, m0, M, lda, kp, k0, as);
-      if constexpr (decltype(lb)::kDirect) lb.issue(Bp, n0, N, ldb, kp, k0, bs);
+      // A row-DMA operand takes its in-bounds extent from the tile's first
+      // column (the operand's end, at this piece's first k).
+      if constexpr (kRowA) la.issue(Ap, m0, kp * lda - m0, lda, kp, k0, as);
+      else if constexpr (decltype(la)::kDirect) la.issue(Ap, m0, M, lda, kp, k0, as);
+      if constexpr (kRowB) lb.issue(Bp, n0, kp * ldb - n0, ldb, kp, k0, bs);
+      else if constexpr (decltype(lb)::kDirect) lb.issue(Bp, n0, N, ldb, kp, k0, bs);
       if constexpr (!decltype(la)::kDirect) la.load(Ap, m0, M, lda, kp, k0);
       if constexpr (!decltype(lb)::kDirect) lb.load(Bp, n0, N, ldb, kp, k0);
     };
@@ -1187,51 +1259,99 @@ __global__ __launch_bounds__(kThreads, 1) void kernel(const double* __restrict__
     }
     publish();
     hpd::f64x2 a[2][FM], b[2][FN];
+    // B of half 0 first: the loop's first MFMAs then wait on the same
+    // in-order LDS counts as after a slice of the three-stage loop.
 #pragma unroll
-    for (int i = 0; i < FM; ++i) {
-      a[0][i] = *reinterpret_cast<const hpd::f64x2*>(&As0[a_read0 + 16 * i * S]);
-      a[1][i] = *reinterpret_cast<const hpd::f64x2*>(&As0[a_read1 + 16 * i * S]);
-    }
+    for (int j = 0; j < FN; ++j) b[0][j] = frag_b(Bs0, 0, j);
+    __builtin_amdgcn_sched_barrier(0);
 #pragma unroll
-    for (int j = 0; j < FN; ++j) {
-      b[0][j] = *reinterpret_cast<const hpd::f64x2*>(&Bs0[b_read0 + 16 * j * S]);
-      b[1][j] = *reinterpret_cast<const hpd::f64x2*>(&Bs0[b_read1 + 16 * j * S]);
-    }
-    // Slice s as in the fp32 kernel: into (as, bs), fragments from (an, bn).
-    auto slice = [&](int64_t s, double* as, double* bs, const double* an, const double* bn) {
-      const bool more = s + 1 < slices;
-      if (s + 2 < slices) load_slice((s + 2) * BK, as, bs);
+    for (int i = 0; i < FM; ++i) a[0][i] = frag_a(As0, 0, i);
+    __builtin_amdgcn_sched_barrier(0);
 #pragma unroll
-      for (int h = 0; h < 2; ++h) {
-        const int a_read = h == 0 ? a_read0 : a_read1;
-        const int b_read = h == 0 ? b_read0 : b_read1;
+    for (int i = 0; i < FM; ++i) a[1][i] = frag_a(As0, 1, i);
 #pragma unroll
-        for (int i = 0; i < FM; ++i) {
+    for (int j = 0; j < FN; ++j) b[1][j] = frag_b(Bs0, 1, j);
+    __builtin_amdgcn_sched_barrier(0);
+    auto mfmas = [&](int h, int i) {
 #pragma unroll
-          for (int q = 0; q < 2; ++q)
+      for (int q = 0; q < 2; ++q)
 #pragma unroll
-            for (int j = 0; j < FN; ++j)
-              acc[i][j] = __builtin_amdgcn_mfma_f64_16x16x4f64(a[h][i][q], b[h][j][q], acc[i][j], 0, 0, 0);
-          if (more) a[h][i] = *reinterpret_cast<const hpd::f64x2*>(an + a_read + 16 * i * S);
-        }
-        if (more) {
-#pragma unroll
-          for (int j = 0; j < FN; ++j) b[h][j] = *reinterpret_cast<const hpd::f64x2*>(bn + b_read + 16 * j * S);
-        }
-        if (h == 0 && s + 2 < slices) store_slice(as, bs);
-      }
-      publish();
+        for (int j = 0; j < FN; ++j)
+          acc[i][j] = __builtin_amdgcn_mfma_f64_16x16x4f64(a[h][i][q], b[h][j][q], acc[i][j], 0, 0, 0);
     };
-    // Every wave has read buffer 0 before slice 0 refills it: the barrier
-    // under the loop's guard, and the carried buffers, as in the fp32 kernel.
-    if (slices > 0) __syncthreads();
     const double* an = As1;
     const double* bn = Bs1;
-    for (int64_t s = 0; s < slices; ++s) {
-      const bool odd = s & 1;
-      slice(s, odd ? As1 : As0, odd ? Bs1 : Bs0, an, bn);
-      an = odd ? As1 : As0;
-      bn = odd ? Bs1 : Bs0;
+    if constexpr (kStages == 3) {
+      // The fp32 kernel's three-stage slice: slice s+2 goes into the third
+      // buffer, issued after the first fragment's MFMAs (that fragment's
+      // refill held back one fragment), unconditional refills, and a barrier
+      // that waits only for the LDS-DMA it publishes.
+      auto slice3 = [&](int64_t s, double* as, double* bs, const double* an, const double* bn) {
+#pragma unroll
+        for (int h = 0; h < 2; ++h) {
+#pragma unroll
+          for (int i = 0; i < FM; ++i) {
+            mfmas(h, i);
+            if (h == 0 && i == 0) {
+              if (s + 2 < slices) load_slice((s + 2) * BK, as, bs);
+            } else {
+              if (h == 0 && i == 1) a[0][0] = frag_a(an, 0, 0);
+              a[h][i] = frag_a(an, h, i);
+            }
+            if (i == FM - 1) {
+#pragma unroll
+              for (int j = 0; j < FN; ++j) b[h][j] = frag_b(bn, h, j);
+            }
+            __builtin_amdgcn_sched_barrier(0);
+          }
+        }
+        wait_vmcnt<0>();
+        dma_barrier();
+      };
+      double *a0 = As0, *a1 = As1, *a2 = As2, *b0 = Bs0, *b1 = Bs1, *b2 = Bs2;
+      for (int64_t s = 0; s < slices; ++s) {
+        slice3(s, a2, b2, an, bn);
+        an = a2;
+        bn = b2;
+        double* t = a0;
+        a0 = a1;
+        a1 = a2;
+        a2 = t;
+        t = b0;
+        b0 = b1;
+        b1 = b2;
+        b2 = t;
+      }
+    } else {
+      // Slice s as in the fp32 kernel: into (as, bs), fragments from (an, bn).
+      auto slice = [&](int64_t s, double* as, double* bs, const double* an, const double* bn) {
+        const bool more = s + 1 < slices;
+        if (s + 2 < slices) load_slice((s + 2) * BK, as, bs);
+#pragma unroll
+        for (int h = 0; h < 2; ++h) {
+#pragma unroll
+          for (int i = 0; i < FM; ++i) {
+            mfmas(h, i);
+            if (more) a[h][i] = frag_a(an, h, i);
+          }
+          if (more) {
+#pragma unroll
+            for (int j = 0; j < FN; ++j) b[h][j] = frag_b(bn, h, j);
+          }
+          if (h == 0 && s + 2 < slices) store_slice(as, bs);
+        }
+        publish();
+      };
+      // Every wave has read buffer 0 before slice 0 refills it: the barrier
+      // under the loop's guard, and the carried buffers, as in the fp32
+      // kernel.
+      if (slices > 0) __syncthreads();
+      for (int64_t s = 0; s < slices; ++s) {
+        const bool odd = s & 1;
+        slice(s, odd ? As1 : As0, odd ? Bs1 : Bs0, an, bn);
+        an = odd ? As1 : As0;
+        bn = odd ? Bs1 : Bs0;
+      }
     }
 
     if (slot < 0) {
@@ -1430,8 +1550,8 @@ bool dma_aligned(const T* a, const T* b, const BatchDesc& bd) {
 // rows * ld + k elements from there, a K-strided one k * ld + rows. Both
 // below 2^31 bytes, else the register-staged mode-2 loads serve the product.
 template <bool TA, bool TB>
-bool dma_offsets_fit(int64_t k, int64_t lda, int64_t ldb, int64_t bm, int64_t bn) {
-  auto fits = [](int64_t elements) { return elements < (int64_t(1) << 29); };
+bool dma_offsets_fit(int64_t k, int64_t lda, int64_t ldb, int64_t bm, int64_t bn, int64_t size = 4) {
+  auto fits = [&](int64_t elements) { return elements < (int64_t(1) << 31) / size; };
   const int64_t a_span = TA ? k * lda + bm : bm * lda + k;
   const int64_t b_span = TB ? bn * ldb + k : k * ldb + bn;
   return fits(a_span) && fits(b_span);
@@ -1593,23 +1713,32 @@ void run_f64(hp_ctx* ctx, const double* a, const double* b, double* c, int64_t m
              const BatchDesc& bd, int64_t batch) {
   using namespace f64;
   TileMap tm;
-  prepare(m, n, batch, BM, BN, tm, TA ? m : k, TB ? k : n, n);
+  const int64_t lda = TA ? m : k, ldb = TB ? k : n;
+  prepare(m, n, batch, BM, BN, tm, lda, ldb, n);
   auto fix = fixup_kernel<double, f64x4, Layout>;
   int mode = mode_of(m, n, k, BM, BN, BK);
-  if (!dma_aligned<double, TA, TB>(a, b, bd)) mode = 2;
-  switch (mode) {
-    case 0:
-      launch_split<double, BM, BN>(ctx, kernel<0, false, TA, TB>, kernel<0, true, TA, TB>, fix, kThreads, a, b, c,
-                                   m, n, k, bd, tm, BK, "gemm_f64", false);
-      break;
-    case 1:
-      launch_split<double, BM, BN>(ctx, kernel<1, false, TA, TB>, kernel<1, true, TA, TB>, fix, kThreads, a, b, c,
-                                   m, n, k, bd, tm, BK, "gemm_f64", false);
-      break;
-    default:
-      launch_split<double, BM, BN>(ctx, kernel<2, false, TA, TB>, kernel<2, true, TA, TB>, fix, kThreads, a, b, c,
-                                   m, n, k, bd, tm, BK, "gemm_f64", false);
-  }
+  if (!dma_aligned<double, TA, TB>(a, b, bd) || !dma_offsets_fit<TA, TB>(k, lda, ldb, BM, BN, sizeof(double)))
+    mode = 2;
+  // RowDma64 takes the K-strided operands (A if TA, B unless TB) when each of
+  // their k rows starts 16-byte aligned.
+  auto rows_aligned = [&] {
+    auto aligned = [&](const double* p, const int64_t* strides, int64_t ld) {
+      if (reinterpret_cast<uintptr_t>(p) % 16 != 0 || ld % 2 != 0) return false;
+      for (int d = 0; d < bd.rank; ++d)
+        if (strides[d] % 2 != 0) return false;
+      return true;
+    };
+    return (!TA || aligned(a, bd.a_stride, lda)) && (TB || aligned(b, bd.b_stride, ldb));
+  };
+  auto run = [&](auto whole, auto cut) {
+    launch_split<double, BM, BN>(ctx, whole, cut, fix, kThreads, a, b, c, m, n, k, bd, tm, BK, "gemm_f64", false);
+  };
+  const bool rows = mode != 2 && rows_aligned();
+  if (mode == 0 && rows) run(kernel<0, false, TA, TB, true>, kernel<0, true, TA, TB, true>);
+  else if (mode == 0) run(kernel<0, false, TA, TB, false>, kernel<0, true, TA, TB, false>);
+  else if (mode == 1 && rows) run(kernel<1, false, TA, TB, true>, kernel<1, true, TA, TB, true>);
+  else if (mode == 1) run(kernel<1, false, TA, TB, false>, kernel<1, true, TA, TB, false>);
+  else run(kernel<2, false, TA, TB, false>, kernel<2, true, TA, TB, false>);
 }
 
 }  // namespace
