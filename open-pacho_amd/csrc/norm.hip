@@ -68,16 +68,18 @@ struct Pair {
   T k, t;
 };
 
+// Without branches: k is the IEEE maximum of the exponents (NaN wins, then
+// +inf, and -inf, the zero pair, is its identity); a side whose exponent
+// difference is not finite (the zero pair, or any side once k is +inf or
+// NaN) adds nothing, and a non-finite k keeps t = 0. For finite pairs this is
+// k = max(ka, kb), t = ta 4^(ka-k) + tb 4^(kb-k), added in that order.
 template <typename T>
 __device__ __forceinline__ Pair<T> merge(Pair<T> a, Pair<T> b) {
-  if (isnan(a.k) || isnan(b.k)) return {T(NAN), T(0)};
-  if (isinf(a.k) && a.k > 0) return a;
-  if (isinf(b.k) && b.k > 0) return b;
-  if (isinf(a.k)) return b;  // a is the zero pair
-  if (isinf(b.k)) return a;
-  const T k = a.k > b.k ? a.k : b.k;
-  const T t = dldexp(a.t, 2 * int(a.k - k)) + dldexp(b.t, 2 * int(b.k - k));
-  return {k, t};
+  const T k = __builtin_elementwise_maximum(a.k, b.k);
+  const T da = a.k - k, db = b.k - k;
+  const T ta = isfinite(da) ? dldexp(a.t, 2 * int(da)) : T(0);
+  const T tb = isfinite(db) ? dldexp(b.t, 2 * int(db)) : T(0);
+  return {k, isfinite(k) ? ta + tb : T(0)};
 }
 
 template <typename T>
@@ -254,16 +256,15 @@ __global__ __launch_bounds__(kBlock) void norm_merge_kernel(const T* __restrict_
 // and forms their pair exactly as a wave does for a contiguous chunk (max,
 // exponent, scaled sum of squares), so every element is read from HBM once;
 // pairs then merge across batches, rows of a step, chunks and passes.
+// Branch-free: the NaN-dropping max gives the scale; the scaled sum of
+// squares is formed whatever the max, and a NaN anywhere makes it NaN (for a
+// max of +inf the +inf squares stay +inf, for a max of 0 the other values are
+// zeros), so a NaN sum marks NaN, then a max of +inf or 0 the infinite or the
+// zero pair. frexp of +inf or 0 only feeds sums that these cases discard.
 template <typename T>
 __device__ __forceinline__ Pair<T> lane_pair(const T* v, int n) {
   T m = T(0);
   for (int i = 0; i < n; ++i) m = dmax(m, dabs(v[i]));
-  if (isinf(m) || m == T(0)) {
-    bool nan = false;
-    for (int i = 0; i < n; ++i) nan = nan || isnan(v[i]);
-    if (nan) return {T(NAN), T(0)};
-    return isinf(m) ? Pair<T>{T(INFINITY), T(0)} : Pair<T>{T(-INFINITY), T(0)};
-  }
   const int e = dexponent(m);
   T t = T(0);
   for (int i = 0; i < n; ++i) {
@@ -271,7 +272,8 @@ __device__ __forceinline__ Pair<T> lane_pair(const T* v, int n) {
     t = dfma(s, s, t);
   }
   if (isnan(t)) return {T(NAN), T(0)};
-  return {T(e), t};
+  if (isinf(m)) return {T(INFINITY), T(0)};
+  return m == T(0) ? Pair<T>{T(-INFINITY), T(0)} : Pair<T>{T(e), t};
 }
 
 template <typename T>

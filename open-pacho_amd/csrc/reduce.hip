@@ -40,19 +40,17 @@ struct Combine<T, HP_SUM> {
   }
 };
 
+// IEEE 754-2019 minimum/maximum: NaN if either operand is NaN, -0 < +0.
+// That is the extrema contract above; gfx950 has them as instructions
+// (v_minimum3_f32 / v_maximum3_f32 take three operands, so the compiler
+// folds two elements per instruction).
 template <typename T>
 __device__ __forceinline__ T float_min(T a, T b) {
-  if (isnan(a)) return a;
-  if (isnan(b)) return b;
-  if (a == T(0) && b == T(0)) return signbit(a) ? a : b;
-  return a < b ? a : b;
+  return __builtin_elementwise_minimum(a, b);
 }
 template <typename T>
 __device__ __forceinline__ T float_max(T a, T b) {
-  if (isnan(a)) return a;
-  if (isnan(b)) return b;
-  if (a == T(0) && b == T(0)) return signbit(a) ? b : a;
-  return a > b ? a : b;
+  return __builtin_elementwise_maximum(a, b);
 }
 
 template <typename T>

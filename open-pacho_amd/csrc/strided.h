@@ -74,17 +74,37 @@ __global__ __launch_bounds__(kThreads) void strided_kernel(const typename Op::In
     const int64_t end = begin + rows_per_chunk < reduced ? begin + rows_per_chunk : reduced;
     const In* base = x + o * reduced * inner + col;
     int64_t r = begin + ro;
-    // Full batches: every row of the batch is inside the chunk.
-    for (; r + int64_t(B - 1) * step < end; r += int64_t(B) * step) {
-      In vals[B][V];
+    // Full batches: every row of the batch is inside the chunk. The next
+    // batch's loads are issued before this one is folded (two register sets
+    // that swap roles), so each wave keeps loads in flight while it folds.
+    auto full = [&](int64_t row) { return row + int64_t(B - 1) * step < end; };
+    auto load = [&](int64_t row, In (&vals)[B][V]) {
 #pragma unroll
-      for (int j = 0; j < B; ++j) load_row<In, V>(base + (r + int64_t(j) * step) * inner, vals[j], stream != 0);
+      for (int j = 0; j < B; ++j) load_row<In, V>(base + (row + int64_t(j) * step) * inner, vals[j], stream != 0);
+    };
+    auto fold = [&](const In (&vals)[B][V]) {
 #pragma unroll
       for (int v = 0; v < V; ++v) {
         In column[B];
 #pragma unroll
         for (int j = 0; j < B; ++j) column[j] = vals[j][v];
         acc[v] = Op::fold(acc[v], column);
+      }
+    };
+    if (full(r)) {
+      In set0[B][V], set1[B][V];
+      load(r, set0);
+      for (;;) {
+        int64_t next = r + int64_t(B) * step;
+        if (full(next)) load(next, set1);
+        fold(set0);
+        r = next;
+        if (!full(r)) break;
+        next = r + int64_t(B) * step;
+        if (full(next)) load(next, set0);
+        fold(set1);
+        r = next;
+        if (!full(r)) break;
       }
     }
     if (r < end) {  // last partial batch: rows past the end read as identity
