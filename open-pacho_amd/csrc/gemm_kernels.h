@@ -517,6 +517,126 @@ struct RowDmaLoader {
   }
 };
 
+// 4-byte LDS-DMA: any operand alignment (rows of odd K, views at any element
+// offset) and the edges of mode 2. One instruction fills 64 consecutive
+// dwords of LDS, a quarter of what the 16-byte form moves, so a slice takes
+// four times the instructions (16 per wave for a 256 x 256 tile, against 128
+// MFMAs); their offsets are formed once per slice, so each costs an M0 write
+// and a scalar add. The descriptor's range ends at the operand's last valid
+// element: anything past it loads +0 and nothing outside the operand is read.
+// Rows (columns) past the operand's extent that still lie inside that range
+// hold other data, which reaches only outputs that are never stored; k past
+// the K edge must load +0, which the range gives K-strided operands (their
+// rows past K lie beyond the last valid element) and k-contiguous ones get
+// from lanes that take an offset outside every range in the K-edge slice.
+constexpr unsigned kOutOfRange = 0x80000000u;
+__device__ __forceinline__ void dma4(__amdgpu_buffer_rsrc_t rsrc, void* lds, unsigned voffset, unsigned soffset) {
+  __builtin_amdgcn_raw_ptr_buffer_load_lds(rsrc, (__attribute__((address_space(3))) void*)lds, 4, voffset, soffset, 0,
+                                           0);
+}
+
+// A k-contiguous operand by 4-byte LDS-DMA into DmaLoader's swizzled
+// [row][16 k] layout: instruction i of a wave fills rows 4 g .. 4 g + 3
+// (g = the wave's first group + i); lane l writes row 4 g + l / 16 at slot
+// (l % 16) / 4, element l % 4, so it fetches k = 4 ((l % 16) / 4 ^
+// swizzle(row)) + l % 4. swizzle(row) = ((4 g + l / 16) >> 1) & 3 depends on
+// g only through its parity: two offsets per lane serve every instruction.
+template <int ROWS, int THREADS>
+struct DmaLoader4 {
+  static constexpr int kWaves = THREADS / 64;
+  static constexpr int kLoads = ROWS / 4 / kWaves;  // per wave and slice
+  static_assert(kLoads * 4 * kWaves == ROWS && kLoads % 2 == 0, "whole pairs of 4-row groups per wave");
+  int g0, lane;
+
+  __device__ __forceinline__ void init(int tid) {
+    g0 = kLoads * __builtin_amdgcn_readfirstlane(tid >> 6);
+    lane = tid & 63;
+  }
+  // This lane's k within a slice for row groups of parity `odd`.
+  __device__ __forceinline__ unsigned k_of(int odd) const {
+    const unsigned row = 4 * (g0 + odd) + (lane >> 4), d = lane & 15;
+    return 4 * ((d >> 2) ^ swizzle(row)) + (d & 3);
+  }
+
+  // Element (r, k) of the tile at p[(r0 + r) * ld + k], valid for r0 + r <
+  // rows and k < kp; byte offsets from the tile's first row below 2^31 (host
+  // check).
+  __device__ __forceinline__ void issue(const float* p, int64_t r0, int64_t rows, int64_t ld, int64_t kp, int64_t k0,
+                                        float* buf) const {
+    const int64_t extent = (rows - 1 - r0) * ld + kp;  // elements through the last valid one
+    const __amdgpu_buffer_rsrc_t rsrc =
+        __builtin_amdgcn_make_buffer_rsrc(const_cast<float*>(p + r0 * ld), 0, int(4 * extent), 0x00020000);
+    const unsigned rl = lane >> 4;
+    const unsigned k_even = k_of(0), k_odd = k_of(1);
+    // k at or past kp - k0 (the K-edge slice only) loads +0.
+    const int64_t left = kp - k0;
+    const unsigned kk = left < 16 ? unsigned(left) : 16u;
+    const unsigned v_even = k_even < kk ? 4 * (rl * unsigned(ld) + k_even) : kOutOfRange;
+    const unsigned v_odd = k_odd < kk ? 4 * (rl * unsigned(ld) + k_odd) : kOutOfRange;
+    // A running scalar offset: one register, one add per instruction.
+    unsigned soffset = 4 * (4 * unsigned(g0) * unsigned(ld) + unsigned(k0));
+    const unsigned group = 16 * unsigned(ld);
+#pragma unroll
+    for (int i = 0; i < kLoads; ++i) {
+      dma4(rsrc, buf + 64 * (g0 + i), i % 2 ? v_odd : v_even, soffset);
+      soffset += group;
+    }
+  }
+  __device__ __forceinline__ void commit(float*) const {}
+  static constexpr bool kDirect = true;
+  __device__ __forceinline__ static int64_t origin(int64_t s0, int64_t) { return s0 * 16; }
+};
+
+// A K-strided operand by 4-byte LDS-DMA into RowDmaLoader's [k][row] layout
+// (row stride ROWS + 4): instruction (k, c) fills tile rows 64 c .. 64 c + 63
+// of k row k, lane l fetching row 64 c + l. No lane takes a special offset:
+// k rows past kp lie beyond the descriptor's range.
+template <int ROWS, int THREADS>
+struct RowDma4 {
+  static constexpr int kPerRow = ROWS / 64;  // instructions per k row
+  static constexpr int kWaves = THREADS / 64;
+  static constexpr int kLoads = 16 * kPerRow / kWaves;
+  static_assert(kLoads * kWaves == 16 * kPerRow, "whole k rows per wave");
+  static constexpr int RS = ROWS + 4;
+  static constexpr int kBufFloats = 16 * RS;
+  int t0, lane;
+
+  __device__ __forceinline__ void init(int tid) {
+    t0 = kLoads * __builtin_amdgcn_readfirstlane(tid >> 6);
+    lane = tid & 63;
+  }
+
+  // Element (r, k) at p[k * ld + r0 + r], valid for r0 + r < rows and
+  // k < kp; byte offsets from the tile's first column below 2^31 (host
+  // check).
+  __device__ __forceinline__ void issue(const float* p, int64_t r0, int64_t rows, int64_t ld, int64_t kp, int64_t k0,
+                                        float* buf) const {
+    const int64_t extent = (kp - 1) * ld + rows - r0;  // elements through the last valid one
+    const __amdgpu_buffer_rsrc_t rsrc =
+        __builtin_amdgcn_make_buffer_rsrc(const_cast<float*>(p + r0), 0, int(4 * extent), 0x00020000);
+    // A running scalar offset (t0 is a multiple of kPerRow: the wave's rows
+    // start at column 0): one register, one add per instruction.
+    static_assert(kLoads % kPerRow == 0, "whole k rows per wave");
+    unsigned soffset = 4 * ((unsigned(k0) + unsigned(t0) / kPerRow) * unsigned(ld));
+    const unsigned next_row = 4 * unsigned(ld) - 256 * (kPerRow - 1);
+#pragma unroll
+    for (int i = 0; i < kLoads; ++i) {
+      const unsigned t = t0 + i, k = t / kPerRow, c = t % kPerRow;
+      dma4(rsrc, buf + k * RS + 64 * c, 4 * lane, soffset);
+      soffset += c == kPerRow - 1 ? next_row : 256u;
+    }
+  }
+  __device__ __forceinline__ void commit(float*) const {}
+  static constexpr bool kDirect = true;
+  __device__ __forceinline__ static int64_t origin(int64_t s0, int64_t ld) { return s0 * 16 * ld; }
+  __device__ __forceinline__ static int read_offset(int row0, int lane) {
+    return 4 * (lane >> 4) * RS + row0 + (lane & 15);
+  }
+  __device__ __forceinline__ static hpd::f32x4 read(const float* base, int f) {
+    return hpd::f32x4{base[16 * f], base[16 * f + RS], base[16 * f + 2 * RS], base[16 * f + 3 * RS]};
+  }
+};
+
 // LDS floats per buffer: the row-DMA layout's, else ROWS x the row stride.
 template <class L, bool ROW, int FALLBACK>
 constexpr int buf_floats() {
@@ -537,6 +657,14 @@ using Loader = typename std::conditional<
     KM, PairLoader<ROWS, THREADS, MODE == 1 ? 0 : MODE>,
     typename std::conditional<MODE == 2, StagedLoader<ROWS, THREADS, MODE>,
                               DmaLoader<ROWS, THREADS, MODE == 1 ? 0 : MODE>>::type>::type;
+
+// Loaders of the kernel's operands: K-strided operands by row LDS-DMA (4-byte
+// form when DWORD), other operands by Loader, or DmaLoader4 when DWORD.
+template <bool DWORD, int ROWS, int THREADS>
+using RowLoader = typename std::conditional<DWORD, RowDma4<ROWS, THREADS>, RowDmaLoader<ROWS, THREADS>>::type;
+template <bool DWORD, bool KM, int MODE, int ROWS, int THREADS>
+using FlatLoader =
+    typename std::conditional<DWORD, DmaLoader4<ROWS, THREADS>, Loader<KM, MODE, ROWS, THREADS>>::type;
 
 // Fragment read offset of lane `lane` for tile row `row0 + (lane & 15)`.
 template <bool KM>
@@ -584,10 +712,16 @@ __global__ __launch_bounds__(CFG::kThreads, CFG::kMinBlocks) void kernel(const f
   constexpr int kThreads = CFG::kThreads;
   using L = Layout<CFG>;
   constexpr int SA = lds_stride<TA>(), SB = lds_stride<!TB>();
-  // ROWDMA: K-strided operands (A if TA, B unless TB) arrive by RowDmaLoader.
-  constexpr bool kRowA = TA && ROWDMA && MODE != 2, kRowB = !TB && ROWDMA && MODE != 2;
-  using LA = typename std::conditional<kRowA, RowDmaLoader<BM, kThreads>, Loader<TA, MODE, BM, kThreads>>::type;
-  using LB = typename std::conditional<kRowB, RowDmaLoader<BN, kThreads>, Loader<!TB, MODE, BN, kThreads>>::type;
+  // ROWDMA in modes 0 and 1: K-strided operands (A if TA, B unless TB) arrive
+  // by RowDmaLoader (16-byte rows). In mode 2 both operands arrive by 4-byte
+  // LDS-DMA (RowDma4 for K-strided ones, DmaLoader4 for k-contiguous ones),
+  // else register-staged. K-strided operands by DMA take the [k][row] layout.
+  constexpr bool kDword = ROWDMA && MODE == 2;
+  constexpr bool kRowA = TA && ROWDMA, kRowB = !TB && ROWDMA;
+  using LA = typename std::conditional<kRowA, RowLoader<kDword, BM, kThreads>,
+                                       FlatLoader<kDword, TA, MODE, BM, kThreads>>::type;
+  using LB = typename std::conditional<kRowB, RowLoader<kDword, BN, kThreads>,
+                                       FlatLoader<kDword, !TB, MODE, BN, kThreads>>::type;
   constexpr int kBufA = buf_floats<LA, kRowA, BM * SA>(), kBufB = buf_floats<LB, kRowB, BN * SB>();
   // Slices in LDS, one variable per buffer and operand: three buffers when
   // both operands arrive by LDS-DMA (loads run two slices ahead), else two.
@@ -1585,7 +1719,8 @@ void run_f32_config(hp_ctx* ctx, const float* a, const float* b, float* c, int64
   prepare(m, n, batch, BM, BN, tm, lda, ldb, ldc);
   auto fix = fixup_kernel<float, hpd::f32x4, Layout<CFG>>;
   int mode = mode_of(m, n, k, BM, BN, BK);
-  if (!dma_aligned<float, TA, TB>(a, b, bd) || !dma_offsets_fit<TA, TB>(k, lda, ldb, BM, BN)) mode = 2;
+  const bool fits = dma_offsets_fit<TA, TB>(k, lda, ldb, BM, BN);
+  if (!dma_aligned<float, TA, TB>(a, b, bd) || !fits) mode = 2;
   const bool rows = kRows && mode != 2 && rows_aligned<TA, TB>(a, b, bd, m, n, lda, ldb);
   auto run = [&](auto whole, auto cut, bool moved) {
     launch_split<float, BM, BN>(ctx, whole, cut, fix, T, a, b, c, m, n, k, bd, tm, BK, "gemm_f32", moved);
@@ -1598,6 +1733,9 @@ void run_f32_config(hp_ctx* ctx, const float* a, const float* b, float* c, int64
     run(kernel<CFG, 1, false, TA, TB, kRows>, kernel<CFG, 1, true, TA, TB, kRows>, true);
   } else if (mode == 1) {
     run(kernel<CFG, 1, false, TA, TB, false>, kernel<CFG, 1, true, TA, TB, false>, true);
+  } else if (fits) {
+    // 4-byte LDS-DMA of both operands at any alignment, edges loading +0.
+    run(kernel<CFG, 2, false, TA, TB, true>, kernel<CFG, 2, true, TA, TB, true>, true);
   } else {
     run(kernel<CFG, 2, false, TA, TB, false>, kernel<CFG, 2, true, TA, TB, false>, true);
   }

@@ -539,8 +539,9 @@ def test_bool_gemm_abi_is_or_of_ands(hip):
 @pytest.mark.parametrize("dtype", [np.float32, np.float64])
 def test_batch_strides_off_the_16_byte_grid(hip, dtype):
     """hp_gemm with an A batch stride of m*k + 1 elements: every other batch
-    matrix starts off a 16-byte boundary, so the product must take the
-    register-staged loads, not LDS-DMA (M, N, K would otherwise allow it)."""
+    matrix starts off a 16-byte boundary, so the product must take the 4-byte
+    LDS-DMA of mode 2, not the 16-byte form (M, N, K would otherwise allow
+    it)."""
     from openpacho import _hip_lib
 
     m, n, k, batch = 256, 256, 32, 3
@@ -561,6 +562,26 @@ def test_batch_strides_off_the_16_byte_grid(hip, dtype):
         want = a_i @ b_host.astype(np.float64)
         scale = np.abs(a_i) @ np.abs(b_host.astype(np.float64))
         assert np.all(np.abs(got[i] - want) <= bound * scale + 1e-30), i
+
+
+@pytest.mark.parametrize("dtype", [np.float32, np.float64])
+@pytest.mark.parametrize("batch,m,n,k", [(3, 300, 280, 77), (2, 256, 256, 1001), (4, 129, 513, 33), (2, 520, 260, 3)])
+def test_k_edge_of_adjacent_batch_matrices_contracts_zeros(hip, dtype, batch, m, n, k):
+    """Batched A and B with K off the 16-wide slice grid: in memory each
+    batch matrix's K edge is followed by the next matrix's data (A's next row,
+    B's next batch), which must not enter the contraction; rows and columns
+    past M and N of one batch matrix may hold the next one's data but reach
+    no stored output. Results against float64, bitwise repeatable."""
+    rng = np.random.default_rng(batch * 1000 + k)
+    a = rng.uniform(-1, 1, (batch, m, k)).astype(dtype)
+    b = rng.uniform(-1, 1, (batch, k, n)).astype(dtype)
+    A, B = p.asarray(a, backend=hip), p.asarray(b, backend=hip)
+    got = p.asnumpy(A @ B)
+    np.testing.assert_array_equal(got, p.asnumpy(A @ B))
+    want = a.astype(np.float64) @ b.astype(np.float64)
+    scale = np.abs(a).astype(np.float64) @ np.abs(b).astype(np.float64)
+    bound = (4e-7 if dtype == np.float32 else 8e-16) * np.sqrt(k) * 4
+    assert np.all(np.abs(got - want) <= bound * scale + 1e-30)
 
 
 # Products whose last tile row or column holds at most 8 rows or columns run
