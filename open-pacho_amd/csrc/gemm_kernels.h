@@ -658,10 +658,12 @@ using Loader = typename std::conditional<
     typename std::conditional<MODE == 2, StagedLoader<ROWS, THREADS, MODE>,
                               DmaLoader<ROWS, THREADS, MODE == 1 ? 0 : MODE>>::type>::type;
 
-// Loaders of the kernel's operands: K-strided operands by row LDS-DMA (4-byte
-// form when DWORD), other operands by Loader, or DmaLoader4 when DWORD.
+// Loaders of the kernel's operands: K-strided operands by row LDS-DMA (the
+// 4-byte form when DWORD or for rows other than 1 KB), other operands by
+// Loader, or DmaLoader4 when DWORD.
 template <bool DWORD, int ROWS, int THREADS>
-using RowLoader = typename std::conditional<DWORD, RowDma4<ROWS, THREADS>, RowDmaLoader<ROWS, THREADS>>::type;
+using RowLoader = typename std::conditional<DWORD || ROWS * 4 != 1024, RowDma4<ROWS, THREADS>,
+                                            RowDmaLoader<ROWS, THREADS>>::type;
 template <bool DWORD, bool KM, int MODE, int ROWS, int THREADS>
 using FlatLoader =
     typename std::conditional<DWORD, DmaLoader4<ROWS, THREADS>, Loader<KM, MODE, ROWS, THREADS>>::type;
@@ -1713,15 +1715,18 @@ void run_f32_config(hp_ctx* ctx, const float* a, const float* b, float* c, int64
                     const BatchDesc& bd, int64_t batch, int64_t lda, int64_t ldb, int64_t ldc) {
   using namespace f32;
   constexpr int BM = CFG::BM, BN = CFG::BN, T = CFG::kThreads;
-  // Row LDS-DMA takes 1 KB rows (256-wide tiles) and a K-strided operand.
-  constexpr bool kRows = BM * 4 == 1024 && BN * 4 == 1024 && (TA || !TB);
+  // A K-strided operand (A if TA, B unless TB) goes by row LDS-DMA in modes 0
+  // and 1: the 16-byte form for the 1 KB rows of 256-wide tiles when they are
+  // 16-byte aligned, the 4-byte form for narrower tiles.
+  constexpr bool kRows = TA || !TB;
+  constexpr bool kWide = BM * 4 == 1024 && BN * 4 == 1024;
   TileMap tm;
   prepare(m, n, batch, BM, BN, tm, lda, ldb, ldc);
   auto fix = fixup_kernel<float, hpd::f32x4, Layout<CFG>>;
   int mode = mode_of(m, n, k, BM, BN, BK);
   const bool fits = dma_offsets_fit<TA, TB>(k, lda, ldb, BM, BN);
   if (!dma_aligned<float, TA, TB>(a, b, bd) || !fits) mode = 2;
-  const bool rows = kRows && mode != 2 && rows_aligned<TA, TB>(a, b, bd, m, n, lda, ldb);
+  const bool rows = kRows && mode != 2 && (!kWide || rows_aligned<TA, TB>(a, b, bd, m, n, lda, ldb));
   auto run = [&](auto whole, auto cut, bool moved) {
     launch_split<float, BM, BN>(ctx, whole, cut, fix, T, a, b, c, m, n, k, bd, tm, BK, "gemm_f32", moved);
   };
