@@ -70,9 +70,18 @@ def _resources(lines):
     return kernels
 
 
+# Per-unit flags. The fp32 GEMM units keep MFMA accumulators in VGPRs: with
+# one wave per SIMD (the narrow kernel's four-buffer form, LDS-bound to one
+# workgroup per compute unit) the compiler otherwise put them in AGPRs and
+# copied them to VGPRs and back every slice. The other kernels of these units
+# compile to the same code either way.
+UNIT_FLAGS = {f"gemm_f32_{layout}": ["-mllvm", "-amdgpu-mfma-vgpr-form=1"] for layout in ("nn", "nt", "tn", "tt")}
+
+
 def _compile(source):
     obj = BUILD / (source.stem + ".o")
-    command = [hipcc(), *FLAGS, "-Rpass-analysis=kernel-resource-usage", "-c", str(source), "-o", str(obj)]
+    command = [hipcc(), *FLAGS, *UNIT_FLAGS.get(source.stem, []), "-Rpass-analysis=kernel-resource-usage", "-c",
+               str(source), "-o", str(obj)]
     result = subprocess.run(command, capture_output=True, text=True)
     lines = (result.stdout + result.stderr).splitlines()
     # hipcc's host pass warns that it does not know the packed-fp32 feature.

@@ -1018,22 +1018,20 @@ template <bool KM>
 struct Operand {
   // Issue the LDS-DMA of one slice (16 k from k0) of a 64-row operand whose
   // tile origin is p: KM = false, element (r, k) at p[r * ld + k]; KM = true,
-  // at p[k * ld + r]. Four 1 KB transfers per wave, all in bounds.
+  // at p[k * ld + r]. Four 1 KB transfers per wave, all in bounds, through a
+  // buffer descriptor (byte offsets from p below 2^31, host check).
   __device__ __forceinline__ static void issue(const float* p, int64_t ld, int64_t k0, float* buf, int lane) {
+    const __amdgpu_buffer_rsrc_t rsrc = buffer_rsrc(p);
 #pragma unroll
     for (int c = 0; c < 4; ++c) {
-      const float* src;
-      float* dst;
       if constexpr (KM) {
-        src = p + (k0 + 4 * c + (lane >> 4)) * ld + 4 * (lane & 15);
-        dst = buf + c * kGroup;
+        const unsigned element = (4 * c + (lane >> 4)) * unsigned(ld) + 4 * (lane & 15);
+        dma16(rsrc, buf + c * kGroup, 4 * element, 4 * unsigned(k0 * ld));
       } else {
         const int row = 16 * c + (lane >> 2);
-        src = p + row * ld + k0 + 4 * ((lane & 3) ^ f32::swizzle(row));
-        dst = buf + 256 * c;
+        const unsigned element = row * unsigned(ld) + 4 * ((lane & 3) ^ f32::swizzle(row));
+        dma16(rsrc, buf + 256 * c, 4 * element, 4 * unsigned(k0));
       }
-      __builtin_amdgcn_global_load_lds(static_cast<const void*>(src),
-                                       (__attribute__((address_space(3))) void*)dst, 16, 0, 0);
     }
   }
   // Fragment f (tile rows 16 f + lane % 16): k = 4 (lane / 16) + q in
@@ -1049,20 +1047,30 @@ struct Operand {
   }
 };
 
-// s_waitcnt vmcnt(n), other counters at their maxima.
+// s_waitcnt vmcnt(n), other counters at their maxima (gfx9: vmcnt bits 3:0
+// and 15:14).
 template <int N>
 __device__ __forceinline__ void wait_vm() {
-  static_assert(N >= 0 && N < 16, "vmcnt immediate");
-  __builtin_amdgcn_s_waitcnt(kWaitVmcnt0 | N);
+  static_assert(N >= 0 && N < 64, "vmcnt immediate");
+  __builtin_amdgcn_s_waitcnt((kWaitVmcnt0 & ~0xC00Fu) | (N & 15) | ((N >> 4) << 14));
 }
 
-template <bool TA, bool TB, int KW>
+// NB = 2: two LDS buffers per wave, slice t + 2 goes into slice t's buffer
+// once its fragments are read (two workgroups fit a compute unit). NB = 4:
+// four buffers, slice t + 3 goes into slice t - 1's buffer, which no read
+// can still touch, so no wait precedes it and loads run three slices ahead
+// (for one tile per compute unit, where a wave has no neighbour on its SIMD
+// to cover its waits).
+template <bool TA, bool TB, int KW, int NB>
 __global__ __launch_bounds__(64 * KW) void kernel(const float* __restrict__ A, const float* __restrict__ B,
                                                   float* __restrict__ C, int64_t M, int64_t N, int64_t K,
                                                   BatchDesc bd, TileMap tmap) {
-  // Buffer 0 and 1 of every wave: [KW][A slice, B slice].
+  static_assert(NB == 2 || NB == 4, "two or four buffers per wave");
+  // Buffers of every wave: [KW][A slice, B slice].
   __shared__ __attribute__((aligned(16))) float L0[KW * kSlice];
   __shared__ __attribute__((aligned(16))) float L1[KW * kSlice];
+  __shared__ __attribute__((aligned(16))) float L2[NB == 4 ? KW * kSlice : 4];
+  __shared__ __attribute__((aligned(16))) float L3[NB == 4 ? KW * kSlice : 4];
   using OA = Operand<TA>;   // A is K-strided when transposed
   using OB = Operand<!TB>;  // B is K-strided unless transposed
   const int lane = threadIdx.x & 63;
@@ -1104,6 +1112,56 @@ __global__ __launch_bounds__(64 * KW) void kernel(const float* __restrict__ A, c
     }
   };
 
+  if constexpr (NB == 4) {
+    // Slices 0-2 in flight; slice 0 must land before its fragments are read.
+    float* const b2 = L2 + wave * kSlice;
+    float* const b3 = L3 + wave * kSlice;
+    if (count > 0) issue(0, b0);
+    if (count > 1) issue(1, b1);
+    if (count > 2) {
+      issue(2, b2);
+      wait_vm<16>();
+    } else {
+      wait_vm<0>();
+    }
+    read(b0, a0, b0f);
+    // Slice t: slice t + 3 into the buffer of slice t - 1 (pd), wait until
+    // slice t + 1 has landed (only t + 2 and t + 3 may be in flight), read
+    // its fragments, then the MFMAs of slice t. The buffers rotate.
+    auto slice4 = [&](int64_t t, float* pd, const float* nxt, const hpd::f32x4* fa, const hpd::f32x4* fb,
+                      hpd::f32x4* na, hpd::f32x4* nb) {
+      if (t + 3 < count) {
+        issue(t + 3, pd);
+        wait_vm<16>();
+      } else {
+        wait_vm<0>();
+      }
+      read(nxt, na, nb);
+#pragma unroll
+      for (int i = 0; i < 4; ++i)
+#pragma unroll
+        for (int q = 0; q < 4; ++q)
+#pragma unroll
+          for (int j = 0; j < 4; ++j)
+            acc[i][j] = __builtin_amdgcn_mfma_f32_16x16x4f32(fa[i][q], fb[j][q], acc[i][j], 0, 0, 0);
+    };
+    float *c0 = b0, *c1 = b1, *c2 = b2, *c3 = b3;  // buffers of slices t .. t + 3
+    auto rotate = [&] {
+      float* x = c0;
+      c0 = c1;
+      c1 = c2;
+      c2 = c3;
+      c3 = x;
+    };
+    int64_t t = 0;
+    for (; t + 1 < count; t += 2) {
+      slice4(t, c3, c1, a0, b0f, a1, b1f);
+      rotate();
+      slice4(t + 1, c3, c1, a1, b1f, a0, b0f);
+      rotate();
+    }
+    if (t < count) slice4(t, c3, c1, a0, b0f, a1, b1f);
+  } else {
   if (count > 0) issue(0, b0);
   if (count > 1) issue(1, b1);
   wait_vm<0>();
@@ -1134,6 +1192,7 @@ __global__ __launch_bounds__(64 * KW) void kernel(const float* __restrict__ A, c
     slice(t + 1, b1, b0, a1, b1f, a0, b0f);
   }
   if (t < count) slice(t, b0, b1, a0, b0f, a1, b1f);
+  }
 
   // Sum the KW accumulator tiles in wave order: waves [0, KW/2) stage theirs
   // in L0, the rest in L1 (16 KB each), then every thread adds whole
@@ -1777,7 +1836,8 @@ template <bool TA, bool TB>
 bool narrow_fits(const float* a, const float* b, const BatchDesc& bd, int64_t m, int64_t n, int64_t k, int64_t lda,
                  int64_t ldb) {
   return m % narrow::T == 0 && n % narrow::T == 0 && k % 16 == 0 && k > 0 && lda % 4 == 0 && ldb % 4 == 0 &&
-         dma_aligned<float, TA, TB>(a, b, bd) && rows_aligned<TA, TB>(a, b, bd, m, n, lda, ldb);
+         dma_aligned<float, TA, TB>(a, b, bd) && rows_aligned<TA, TB>(a, b, bd, m, n, lda, ldb) &&
+         dma_offsets_fit<TA, TB>(k, lda, ldb, narrow::T, narrow::T);
 }
 
 // Narrow tiles for short products that the 64 x 64 tiles spread over the
@@ -1806,7 +1866,13 @@ void run_f32_narrow(hp_ctx* ctx, const float* a, const float* b, float* c, int64
                     const BatchDesc& bd, int64_t batch, int64_t lda, int64_t ldb, int64_t ldc) {
   TileMap tm;
   prepare(m, n, batch, narrow::T, narrow::T, tm, lda, ldb, ldc);
-  narrow::kernel<TA, TB, kNarrowWaves><<<tm.total, 64 * kNarrowWaves, 0, ctx->stream>>>(a, b, c, m, n, k, bd, tm);
+  // One tile per compute unit: four buffers per wave (loads three slices
+  // ahead, one workgroup per compute unit); more tiles: two, so that two
+  // workgroups share a compute unit.
+  if (tm.total <= ctx->compute_units)
+    narrow::kernel<TA, TB, kNarrowWaves, 4><<<tm.total, 64 * kNarrowWaves, 0, ctx->stream>>>(a, b, c, m, n, k, bd, tm);
+  else
+    narrow::kernel<TA, TB, kNarrowWaves, 2><<<tm.total, 64 * kNarrowWaves, 0, ctx->stream>>>(a, b, c, m, n, k, bd, tm);
   hp::check_launch("gemm_f32");
 }
 

@@ -98,7 +98,7 @@ def test_gemm_lds_reads_keep_their_barriers_and_skip_dma_waits(unit, tmp_path):
         pytest.skip("hipcc not available")
     source = build.CSRC / f"{unit}.hip"
     asm = tmp_path / f"{unit}.s"
-    flags = [f for f in build.FLAGS if f != "-Wall"]
+    flags = [f for f in build.FLAGS if f != "-Wall"] + build.UNIT_FLAGS.get(unit, [])
     subprocess.run([build.hipcc(), *flags, "--cuda-device-only", "-S", str(source), "-o", str(asm)], check=True,
                    capture_output=True)
     kernel, previous, barriers, checked = None, "", {}, set()
