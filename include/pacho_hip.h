@@ -8,9 +8,13 @@
  *     available from hp_last_error().
  *   - Sizes and element counts are int64_t; strides are in elements.
  *   - Device pointers are plain `void*` obtained from hp_alloc().
- *   - All device work of one context is ordered on that context's single
- *     non-blocking stream. Entry points that launch kernels return as soon as
- *     the work is enqueued; hp_d2h() and hp_sync() wait for it.
+ *   - All device work of one context is ordered on that context's
+ *     non-blocking stream. (A GEMM may run independent kernels on a second,
+ *     context-owned stream; that stream is forked from and joined back into
+ *     the main one inside the call, so ordering is as if on one stream.)
+ *     Entry points that launch kernels return as soon as the work is
+ *     enqueued; hp_d2h() and hp_sync() wait for it. A context is used from
+ *     one host thread at a time.
  *   - No entry point reads an output buffer before writing it, and none writes
  *     to an input buffer.
  *
@@ -79,8 +83,9 @@ int hp_device_info(int device, char* name, int64_t name_len, char* arch, int64_t
 
 /* ---- context, memory, transfers ------------------------------------------ */
 
-/* Create a context on `device`: one non-blocking stream, a stream-ordered
- * caching pool and a hipRTC module table.
+/* Create a context on `device`: a non-blocking stream (and a second one for
+ * work forked and joined inside a call), a stream-ordered caching pool and a
+ * hipRTC module table.
  * Replaces: _cuda.py:138-199 (CUDABackend.__init__). */
 int hp_init(int device, hp_ctx** out);
 

@@ -70,6 +70,14 @@ struct hp_event {
 struct hp_ctx {
   int device = 0;
   hipStream_t stream = nullptr;
+  // A second stream (default priority) for independent work that may overlap
+  // the main stream's (the edge strips of a GEMM beside its tiled kernels),
+  // forked and joined with these events; the main stream always waits for it
+  // before its next work, so callers see one stream. A context's calls are
+  // not to be made from several host threads at once (the GEMM points
+  // `stream` at `side` while it queues the strips).
+  hipStream_t side = nullptr;
+  hipEvent_t fork = nullptr, join = nullptr;
   int compute_units = 0;
   std::recursive_mutex mutex;
   // Stream-ordered caching pool: size class -> free blocks.

@@ -4,6 +4,8 @@
 // so that the variants build in parallel; gemm.hip holds the entry points.
 #pragma once
 
+#include <vector>
+
 #include "common.h"
 
 namespace hpgemm {
@@ -41,10 +43,12 @@ constexpr int kEdgeMax = 8;
 struct Strides {
   int64_t as_r, as_k, bs_k, bs_n;
 };
+// Their pool temporaries go to `deferred` (when given) for the caller to free
+// once the strips' stream has been joined.
 void edge_rows_f32(hp_ctx* ctx, const float* a, const float* b, float* c, int rows, int64_t n, int64_t k,
-                   const Strides& st, int64_t ldc);
+                   const Strides& st, int64_t ldc, std::vector<void*>* deferred = nullptr);
 void edge_cols_f32(hp_ctx* ctx, const float* a, const float* b, float* c, int64_t m, int cols, int64_t k,
-                   const Strides& st, int64_t ldc);
+                   const Strides& st, int64_t ldc, std::vector<void*>* deferred = nullptr);
 
 // C[b] = op(A[b']) @ op(B[b'']) for b < batch, m x n x k, row-major; op(A)
 // is A stored [k][m] for layout t?, op(B) is B stored [n][k] for ?t.

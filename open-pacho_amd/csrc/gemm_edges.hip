@@ -171,7 +171,7 @@ __global__ __launch_bounds__(kThreads) void cols_kernel(const float* __restrict_
 namespace hpgemm {
 
 void edge_rows_f32(hp_ctx* ctx, const float* a, const float* b, float* c, int rows, int64_t n, int64_t k,
-                   const Strides& st, int64_t ldc) {
+                   const Strides& st, int64_t ldc, std::vector<void*>* deferred) {
   hp::require(rows >= 1 && rows <= kEdgeMax && n >= 1 && k >= 1, "internal: edge rows strip out of range");
   const int64_t col_blocks = hp::ceil_div(n, kThreads);
   // About 1,024 workgroups stream B (latency-bound loads: 4097 x 2049 x 3001
@@ -193,11 +193,12 @@ void edge_rows_f32(hp_ctx* ctx, const float* a, const float* b, float* c, int ro
   hp::check_launch("gemm_edge_rows");
   rows_merge_kernel<<<hp::ceil_div(rows * n, kThreads), kThreads, 0, ctx->stream>>>(partial, c, rows, n, chunks, ldc);
   hp::check_launch("gemm_edge_rows_merge");
-  hp::scratch_free(ctx, partial);
+  if (deferred) deferred->push_back(partial);
+  else hp::scratch_free(ctx, partial);
 }
 
 void edge_cols_f32(hp_ctx* ctx, const float* a, const float* b, float* c, int64_t m, int cols, int64_t k,
-                   const Strides& st, int64_t ldc) {
+                   const Strides& st, int64_t ldc, std::vector<void*>* deferred) {
   hp::require(cols >= 1 && cols <= kEdgeMax && m >= 1 && k >= 1, "internal: edge columns strip out of range");
   float* packed = static_cast<float*>(hp::scratch_alloc(ctx, size_t(cols) * k * sizeof(float)));
   pack_columns_kernel<<<hp::ceil_div(cols * k, kThreads), kThreads, 0, ctx->stream>>>(b, packed, cols, k, st.bs_k,
@@ -210,7 +211,8 @@ void edge_cols_f32(hp_ctx* ctx, const float* a, const float* b, float* c, int64_
     cols_kernel<false><<<grid, kThreads, 0, ctx->stream>>>(a, packed, c, m, cols, k, st.as_r, st.as_k, ldc);
   }
   hp::check_launch("gemm_edge_cols");
-  hp::scratch_free(ctx, packed);
+  if (deferred) deferred->push_back(packed);
+  else hp::scratch_free(ctx, packed);
 }
 
 }  // namespace hpgemm

@@ -48,6 +48,8 @@
 
 #include "gemm.h"
 
+#include <vector>
+
 namespace {
 
 using hpgemm::BatchDesc;
@@ -302,14 +304,6 @@ __device__ __forceinline__ void dma_barrier() { __builtin_amdgcn_s_barrier(); }
 __device__ __forceinline__ void lds_barrier() {
   __builtin_amdgcn_s_waitcnt(0xC07F);  // lgkmcnt(0)
   __builtin_amdgcn_s_barrier();
-}
-
-// LDS-DMA instructions per wave and slice of two direct loaders (0 when
-// either one is register-staged).
-template <class LA, class LB>
-constexpr int slice_loads() {
-  if constexpr (LA::kDirect && LB::kDirect) return LA::kLoads + LB::kLoads;
-  else return 0;
 }
 
 // ------------------------------------------------------------------ fp32 ----
@@ -728,7 +722,6 @@ __global__ __launch_bounds__(CFG::kThreads, CFG::kMinBlocks) void kernel(const f
   // Slices in LDS, one variable per buffer and operand: three buffers when
   // both operands arrive by LDS-DMA (loads run two slices ahead), else two.
   constexpr int kStages = LA::kDirect && LB::kDirect ? 3 : 2;
-  constexpr int kSliceLoads = slice_loads<LA, LB>();
   __shared__ __attribute__((aligned(16))) float As0[kBufA];
   __shared__ __attribute__((aligned(16))) float As1[kBufA];
   __shared__ __attribute__((aligned(16))) float As2[kStages == 3 ? kBufA : 4];
@@ -1423,10 +1416,10 @@ __global__ __launch_bounds__(kThreads, 1) void kernel(const double* __restrict__
     // registers into spills (transposed A: 23 -> 209 spilled VGPRs).
     auto load_slice = [&](int64_t k0, double* as, double* bs) {
       // A row-DMA operand takes its in-bounds extent from the tile's first
-      // column (the operand's end, at this piece's first k).
-      if constexpr (kRowA) la.issue(Ap, m0, kp * lda - m0, lda, kp, k0, as);
+      // column: through the last valid element, row kp - 1, column M (N) - 1.
+      if constexpr (kRowA) la.issue(Ap, m0, (kp - 1) * lda + M - m0, lda, kp, k0, as);
       else if constexpr (decltype(la)::kDirect) la.issue(Ap, m0, M, lda, kp, k0, as);
-      if constexpr (kRowB) lb.issue(Bp, n0, kp * ldb - n0, ldb, kp, k0, bs);
+      if constexpr (kRowB) lb.issue(Bp, n0, (kp - 1) * ldb + N - n0, ldb, kp, k0, bs);
       else if constexpr (decltype(lb)::kDirect) lb.issue(Bp, n0, N, ldb, kp, k0, bs);
       if constexpr (!decltype(la)::kDirect) la.load(Ap, m0, M, lda, kp, k0);
       if constexpr (!decltype(lb)::kDirect) lb.load(Bp, n0, N, ldb, kp, k0);
@@ -1693,6 +1686,15 @@ Split plan_split(int64_t total, int64_t slices, int64_t cus, int64_t per_cu) {
   return sp;
 }
 
+// Points ctx->stream at the side stream for the lifetime of the object (the
+// launch helpers enqueue on ctx->stream), restoring the main stream after.
+struct SideStream {
+  hp_ctx* ctx;
+  hipStream_t main;
+  explicit SideStream(hp_ctx* c) : ctx(c), main(c->stream) { ctx->stream = ctx->side; }
+  ~SideStream() { ctx->stream = main; }
+};
+
 // Launches the whole-tile kernel over the complete rounds and, if tiles are
 // cut, the stream-K kernel and the fixup over a pooled workspace.
 template <typename T, int BM, int BN, typename Whole, typename Cut, typename Fix>
@@ -1908,9 +1910,24 @@ void run_f32(hp_ctx* ctx, const float* a, const float* b, float* c, int64_t m, i
       const int64_t mt = split_rows ? m - rows : m, nt = split_cols ? n - cols : n;
       // op(A)(r, k) and op(B)(k, n) in the stored layouts.
       const hpgemm::Strides st{TA ? 1 : k, TA ? m : 1, TB ? 1 : n, TB ? k : 1};
+      // The strips write outputs the tiles do not and read only A and B, so
+      // they run on the side stream beside the tiled kernels: a few dozen
+      // small workgroups among the tiles' one per compute unit cost the
+      // tiles little, where run after them they and the launch gaps between
+      // them added a tenth to the product. The main stream waits for them
+      // before its next work; their pool temporaries are freed after that.
+      std::vector<void*> deferred;
+      HP_CHECK(hipEventRecord(ctx->fork, ctx->stream));
+      HP_CHECK(hipStreamWaitEvent(ctx->side, ctx->fork, 0));
+      {
+        SideStream on_side(ctx);
+        if (split_cols) hpgemm::edge_cols_f32(ctx, a, b + nt * st.bs_n, c + nt, mt, int(cols), k, st, n, &deferred);
+        if (split_rows) hpgemm::edge_rows_f32(ctx, a + mt * st.as_r, b, c + mt * n, int(rows), n, k, st, n, &deferred);
+      }
       run_f32_tiles<TA, TB>(ctx, a, b, c, mt, nt, k, bd, 1, lda, ldb, n);
-      if (split_cols) hpgemm::edge_cols_f32(ctx, a, b + nt * st.bs_n, c + nt, mt, int(cols), k, st, n);
-      if (split_rows) hpgemm::edge_rows_f32(ctx, a + mt * st.as_r, b, c + mt * n, int(rows), n, k, st, n);
+      HP_CHECK(hipEventRecord(ctx->join, ctx->side));
+      HP_CHECK(hipStreamWaitEvent(ctx->stream, ctx->join, 0));
+      for (void* p : deferred) hp::scratch_free(ctx, p);
       return;
     }
   }

@@ -173,9 +173,15 @@ int hp_init(int device, hp_ctx** out) {
     ctx->compute_units = prop.multiProcessorCount;
     ctx->pool_limit = static_cast<size_t>(prop.totalGlobalMem / 4);
     HP_CHECK(hipStreamCreateWithFlags(&ctx->stream, hipStreamNonBlocking));
+    HP_CHECK(hipStreamCreateWithFlags(&ctx->side, hipStreamNonBlocking));
+    HP_CHECK(hipEventCreateWithFlags(&ctx->fork, hipEventDisableTiming));
+    HP_CHECK(hipEventCreateWithFlags(&ctx->join, hipEventDisableTiming));
     *out = ctx;
   });
   if (status != HP_OK && ctx != nullptr) {
+    if (ctx->join) (void)hipEventDestroy(ctx->join);
+    if (ctx->fork) (void)hipEventDestroy(ctx->fork);
+    if (ctx->side) (void)hipStreamDestroy(ctx->side);
     if (ctx->stream) (void)hipStreamDestroy(ctx->stream);
     delete ctx;
     if (out) *out = nullptr;
@@ -189,10 +195,14 @@ int hp_destroy(hp_ctx* ctx) {
     hp::set_device(ctx->device);
     std::lock_guard<std::recursive_mutex> lock(ctx->mutex);
     HP_CHECK(hipStreamSynchronize(ctx->stream));
+    HP_CHECK(hipStreamSynchronize(ctx->side));
     for (auto& entry : ctx->free_blocks) HP_CHECK(hipFree(entry.second));
     for (auto& entry : ctx->live) HP_CHECK(hipFree(entry.first));
     ctx->free_blocks.clear();
     ctx->live.clear();
+    HP_CHECK(hipEventDestroy(ctx->join));
+    HP_CHECK(hipEventDestroy(ctx->fork));
+    HP_CHECK(hipStreamDestroy(ctx->side));
     HP_CHECK(hipStreamDestroy(ctx->stream));
     ctx->stream = nullptr;
   });
