@@ -333,6 +333,12 @@ using Big = Tile<256, 256, 2, 4, 1>;
 // 128 x 128, 4 waves of 64 x 64, two workgroups per compute unit: four times
 // the tiles of Big, for products whose Big tiles do not fill the chip.
 using Small = Tile<128, 128, 2, 2, 2>;
+// 256 x 192, 8 waves of 128 x 48, one workgroup per compute unit: a third
+// more tiles than Big, for products whose Big tiles would fill part of a
+// round (stream-K and a fixup) while these fill it whole. Both operands by
+// 4-byte LDS-DMA (mode 2 kernels only: 192-row slices are not whole 16-byte
+// DMA chunks per wave).
+using Wide = Tile<256, 192, 2, 4, 1>;
 
 // gfx950 LDS banks, measured with SQ_LDS_BANK_CONFLICT on probe kernels: a
 // ds_read_b128 serves its 64 lanes in four groups of 16 (lane bit 5 and the
@@ -1878,11 +1884,47 @@ void run_f32_narrow(hp_ctx* ctx, const float* a, const float* b, float* c, int64
   hp::check_launch("gemm_f32");
 }
 
+// Wide tiles where Big's fill part of one round (all of them then cut into
+// stream-K runs and summed by a fixup launch) while Wide's fill 7/8 of one
+// round or more, whole. Measured on one MI355X, TFLOP/s Wide / Big:
+//   4096 x 3001 x 2049 128.9 / 121.0, 2048 x 6000 x 1024 126.6 / 118.5,
+//   4000 x 2900 x 3001 123.3 / 119.7, 4096 x 3072 x 2048 133.3 / 133.6;
+// where Big's tiles span more than one round only the last is cut and the
+// whole-tile Wide product loses (4096 x 6000 x 1024, two Wide rounds:
+// 127.5 / 129.2), and so do 256 x 128 tiles against Big's cut ones (4096 x
+// 2048 x 3008: 129.3 / 136.5).
+inline bool wide_tiles(hp_ctx* ctx, int64_t m, int64_t n, int64_t batch) {
+  using f32::Big;
+  using f32::Wide;
+  const int64_t cus = ctx->compute_units;
+  const int64_t big = hp::ceil_div(m, Big::BM) * hp::ceil_div(n, Big::BN) * batch;
+  const int64_t wide = hp::ceil_div(m, Wide::BM) * hp::ceil_div(n, Wide::BN) * batch;
+  return big < cus && wide <= cus && 8 * wide >= 7 * cus;
+}
+
+// Whole Wide tiles, one launch: 4-byte LDS-DMA at any alignment, edges load
+// +0 (the mode 2 kernel), no stream-K.
+template <bool TA, bool TB>
+void run_f32_wide(hp_ctx* ctx, const float* a, const float* b, float* c, int64_t m, int64_t n, int64_t k,
+                  const BatchDesc& bd, int64_t batch, int64_t lda, int64_t ldb, int64_t ldc) {
+  using namespace f32;
+  TileMap tm;
+  prepare(m, n, batch, Wide::BM, Wide::BN, tm, lda, ldb, ldc);
+  Split sp{};
+  sp.dp_tiles = tm.total;
+  sp.slices = hp::ceil_div(k, BK);
+  kernel<Wide, 2, false, TA, TB, true><<<tm.total, Wide::kThreads, 0, ctx->stream>>>(a, b, c, m, n, k, bd, tm, sp);
+  hp::check_launch("gemm_f32");
+}
+
 template <bool TA, bool TB>
 void run_f32_tiles(hp_ctx* ctx, const float* a, const float* b, float* c, int64_t m, int64_t n, int64_t k,
                    const BatchDesc& bd, int64_t batch, int64_t lda, int64_t ldb, int64_t ldc) {
   if (narrow_tiles(ctx, m, n, k, batch) && narrow_fits<TA, TB>(a, b, bd, m, n, k, lda, ldb)) {
     run_f32_narrow<TA, TB>(ctx, a, b, c, m, n, k, bd, batch, lda, ldb, ldc);
+  } else if (wide_tiles(ctx, m, n, batch) &&
+             dma_offsets_fit<TA, TB>(k, lda, ldb, f32::Wide::BM, f32::Wide::BN)) {
+    run_f32_wide<TA, TB>(ctx, a, b, c, m, n, k, bd, batch, lda, ldb, ldc);
   } else if (small_tiles(ctx, m, n, k, batch)) {
     run_f32_config<f32::Small, TA, TB>(ctx, a, b, c, m, n, k, bd, batch, lda, ldb, ldc);
   } else {

@@ -398,6 +398,44 @@ def test_narrow_tiles_against_float64_and_deterministic(hip, ta, tb, batch, m, n
         np.testing.assert_array_equal(got, eager)
 
 
+# ---- 256 x 192 tiles: products whose 256 x 256 tiles would fill part of
+# one round of the 256 compute units (and be cut into stream-K runs) while
+# the 192-wide tiles fill at least 7/8 of it whole. One launch, both operands
+# by 4-byte LDS-DMA with descriptor-range edges.
+
+WIDE_CASES = [
+    ((), 4096, 3072, 512),  # 192 -> 256 tiles, interior
+    ((), 4000, 2900, 333),  # M, N and K edges
+    ((2,), 2048, 3072, 160),  # batched
+    ((), 2048, 6000, 64),  # short K, N edge of 48 columns
+]
+
+
+@pytest.mark.parametrize("ta,tb", [(False, False), (True, False), (False, True), (True, True)])
+@pytest.mark.parametrize("batch,m,n,k", WIDE_CASES)
+def test_wide_tiles_against_float64_and_deterministic(hip, ta, tb, batch, m, n, k):
+    if batch and (ta or tb):
+        pytest.skip("transposed operands are 2-D")
+    rng = np.random.default_rng(3 * m + n + 13 * k + 2 * ta + tb)
+    left = rng.uniform(-1, 1, batch + ((k, m) if ta else (m, k))).astype(np.float32)
+    right = rng.uniform(-1, 1, (n, k) if tb else (k, n)).astype(np.float32)
+    a, b = p.asarray(left, backend=hip), p.asarray(right, backend=hip)
+    product = p.compile(lambda x, y: (x.T if ta else x) @ (y.T if tb else y))
+    got = p.asnumpy(product(a, b))
+    np.testing.assert_array_equal(got, p.asnumpy(product(a, b)))  # fixed K order: repeatable
+    op_a = (left.T if ta else left).astype(np.float64)
+    op_b = (right.T if tb else right).astype(np.float64)
+    want = op_a @ op_b
+    scale = np.abs(op_a) @ np.abs(op_b)
+    bound = 4e-7 * np.sqrt(k) * 4
+    assert np.all(np.abs(got - want) <= bound * scale + 1e-30)
+    if ta or tb:
+        # The materialized transposes give the same bits (same tiles, same K order).
+        eager = p.asnumpy(p.asarray(np.ascontiguousarray(op_a.astype(np.float32)), backend=hip)
+                          @ p.asarray(np.ascontiguousarray(op_b.astype(np.float32)), backend=hip))
+        np.testing.assert_array_equal(got, eager)
+
+
 # ---- products of private transposes (hp_gemm_layout), reference
 # tests/test_clblast.py:410-440 and tests/test_compiled_layout.py:43-80
 
