@@ -36,11 +36,12 @@ def _kernels(resources, unit):
     return {name: r for name, r in resources.get(unit, {}).items() if "kernel" in name}
 
 
-# Scalar registers that the any-alignment stream-K kernels (two pieces with
-# 4-byte LDS-DMA descriptors each) may spill. An SGPR spill goes to a lane of
-# a VGPR (v_writelane / v_readlane, no memory traffic); in these kernels the
-# spill code sits before and after the K loops.
-FP32_SGPR_SPILL_LIMIT = 8
+# Scalar registers that the any-alignment stream-K kernels (two pieces, each
+# with the state of both LDS-DMA forms: 16-byte for whole K slices, 4-byte
+# for the K edge) may spill. An SGPR spill goes to a lane of a VGPR
+# (v_writelane / v_readlane, no memory traffic); in these kernels the spill
+# code sits before and after the K loops.
+FP32_SGPR_SPILL_LIMIT = 12
 
 
 def test_fp32_gemm_kernels_do_not_spill_and_keep_two_waves(resources):

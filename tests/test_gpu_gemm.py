@@ -436,6 +436,32 @@ def test_wide_tiles_against_float64_and_deterministic(hip, ta, tb, batch, m, n, 
         np.testing.assert_array_equal(got, eager)
 
 
+# ---- odd K (a K-edge slice): the whole K slices of products at least one
+# tile tall and wide load by 16-byte LDS-DMA from 4-byte aligned addresses,
+# the K-edge slice by 4-byte LDS-DMA that zero-fills past K. 256 x 256 tiles
+# in one whole round, 256 x 256 tiles cut by stream-K, 128 x 128 tiles.
+
+ODD_K_CASES = [(4096, 4096, 161), (1024, 1024, 4097), (520, 300, 2049)]
+
+
+@pytest.mark.parametrize("ta,tb", [(False, False), (True, False), (False, True), (True, True)])
+@pytest.mark.parametrize("m,n,k", ODD_K_CASES)
+def test_odd_k_products_against_float64_and_deterministic(hip, ta, tb, m, n, k):
+    rng = np.random.default_rng(m + 7 * n + 3 * k + 2 * ta + tb)
+    left = rng.uniform(-1, 1, (k, m) if ta else (m, k)).astype(np.float32)
+    right = rng.uniform(-1, 1, (n, k) if tb else (k, n)).astype(np.float32)
+    a, b = p.asarray(left, backend=hip), p.asarray(right, backend=hip)
+    product = p.compile(lambda x, y: (x.T if ta else x) @ (y.T if tb else y))
+    got = p.asnumpy(product(a, b))
+    np.testing.assert_array_equal(got, p.asnumpy(product(a, b)))
+    op_a = (left.T if ta else left).astype(np.float64)
+    op_b = (right.T if tb else right).astype(np.float64)
+    want = op_a @ op_b
+    scale = np.abs(op_a) @ np.abs(op_b)
+    bound = 4e-7 * np.sqrt(k) * 4
+    assert np.all(np.abs(got - want) <= bound * scale + 1e-30)
+
+
 # ---- products of private transposes (hp_gemm_layout), reference
 # tests/test_clblast.py:410-440 and tests/test_compiled_layout.py:43-80
 
