@@ -418,19 +418,21 @@ struct PairLoader {
   __device__ __forceinline__ static int64_t origin(int64_t s0, int64_t ld) { return s0 * 16 * ld; }
 };
 
-// A k-contiguous operand in modes 0 and 1, rows 16-byte aligned (host
-// check): its K slice goes from global memory straight into LDS with
-// global_load_lds_dwordx4, without registers or ds_write. LDS-DMA writes
-// 16 bytes per lane at consecutive addresses, so wave w fills 16-row chunks
-// 2w and 2w + 1 (1 KB each) and lane l fetches the global group that the
-// swizzle places at its position: row 16c + l / 4, k group (l % 4) ^
-// swizzle(row). Completion is tracked by vmcnt; kernels wait for vmcnt(0)
-// before the barrier that publishes a slice. Every row read is in bounds.
+// A k-contiguous operand in modes 0 and 1 (and the whole K slices of mode
+// 2): its K slice goes from global memory straight into LDS with 16-byte
+// LDS-DMA, without registers or ds_write. LDS-DMA writes 16 bytes per lane
+// at consecutive addresses, so a wave fills whole 16-row chunks (1 KB each;
+// kChunks per wave, the last waves fewer when the chunks do not divide
+// evenly) and lane l fetches the global group that the swizzle places at its
+// position: row 16c + l / 4, k group (l % 4) ^ swizzle(row). Completion is
+// tracked by vmcnt; kernels wait for vmcnt(0) before the barrier that
+// publishes a slice. Every row read is in bounds.
 template <int ROWS, int THREADS, int MODE>
 struct DmaLoader {
   static_assert(MODE == 0, "in-bounds rows only: mode 1 moves edge tiles inside, mode 2 stages");
-  static constexpr int kChunks = ROWS / 16 / (THREADS / 64);  // 16-row chunks per wave
-  static_assert(kChunks * 16 * (THREADS / 64) == ROWS, "whole 16-row chunks per wave");
+  static constexpr int kRowChunks = ROWS / 16;
+  static_assert(kRowChunks * 16 == ROWS, "whole 16-row chunks");
+  static constexpr int kChunks = (kRowChunks + THREADS / 64 - 1) / (THREADS / 64);  // per wave, at most
   int chunk0, lane;
 
   __device__ __forceinline__ void init(int tid) {
@@ -449,6 +451,7 @@ struct DmaLoader {
 #pragma unroll
     for (int i = 0; i < kChunks; ++i) {
       const int c = chunk0 + i;
+      if (kRowChunks % (THREADS / 64) != 0 && c >= kRowChunks) break;  // wave-uniform
       const unsigned row = 16 * c + (lane >> 2);
       const unsigned element = row * unsigned(ld) + 4 * ((lane & 3) ^ swizzle(row));
       dma16(rsrc, buf + 256 * c, 4 * element, 4 * unsigned(k0));
@@ -473,16 +476,18 @@ struct StagedLoader : SliceLoader<float, ROWS, false, MODE, THREADS> {
 };
 
 // A K-strided operand ([k][rows] in memory: B, or A transposed) in modes 0
-// and 1 when each of its k rows starts 16-byte aligned (host check): one
-// LDS-DMA per k row moves the tile's ROWS floats (1 KB) into LDS, stored
-// [k][row] at a row stride of RS floats. No registers, no ds_write and no
-// wait in the middle of the slice, against the register-staged pair loader
-// (8192^3: the staged B path costs 3.7% of peak, its DMA 1%). A fragment is
-// then four 4-byte reads, rows 4 (lane / 16) + q: the 16-byte pad puts the
-// four lane groups on disjoint bank sets (4 RS = 1040 dwords = 16 mod 64).
+// and 1 (and the whole K slices of mode 2): one 16-byte LDS-DMA per k row
+// moves the tile's ROWS floats (1 KB for 256 rows; narrower tiles leave the
+// lanes past ROWS / 4 idle) into LDS, stored [k][row] at a row stride of RS
+// floats. No registers, no ds_write and no wait in the middle of the slice,
+// against the register-staged pair loader (8192^3: the staged B path costs
+// 3.7% of peak, its DMA 1%). A fragment is then four 4-byte reads, rows 4
+// (lane / 16) + q: the 16-byte pad puts the four lane groups on disjoint
+// bank sets (4 RS = 16 mod 64 dwords for RS = 132, 196, 260).
 template <int ROWS, int THREADS>
 struct RowDmaLoader {
-  static_assert(ROWS * 4 == 1024, "one 1 KB LDS-DMA per k row");
+  static_assert(ROWS % 64 == 0 && ROWS <= 256, "16-byte lanes of one LDS-DMA per k row");
+  static constexpr int kLanes = ROWS / 4;
   static constexpr int kRowsPerWave = 16 / (THREADS / 64);
   static_assert(kRowsPerWave * (THREADS / 64) == 16, "whole k rows per wave");
   static constexpr int RS = ROWS + 4;
@@ -502,6 +507,7 @@ struct RowDmaLoader {
   }
   // The same from a descriptor whose base is the tile's first column.
   __device__ __forceinline__ void issue(__amdgpu_buffer_rsrc_t rsrc, int64_t ld, int64_t k0, float* buf) const {
+    if (kLanes < 64 && lane >= kLanes) return;
 #pragma unroll
     for (int i = 0; i < kRowsPerWave; ++i) {
       const unsigned k = k0w + i;
@@ -673,11 +679,11 @@ using Loader = typename std::conditional<
                               DmaLoader<ROWS, THREADS, MODE == 1 ? 0 : MODE>>::type>::type;
 
 // Loaders of the kernel's operands: K-strided operands by row LDS-DMA (the
-// 4-byte form when DWORD or for rows other than 1 KB), other operands by
-// Loader, or DmaLoader4 when DWORD.
+// 4-byte form when DWORD), other operands by Loader, or DmaLoader4 when
+// DWORD.
 template <bool DWORD, int ROWS, int THREADS>
-using RowLoader = typename std::conditional<DWORD || ROWS * 4 != 1024, RowDma4<ROWS, THREADS>,
-                                            RowDmaLoader<ROWS, THREADS>>::type;
+using RowLoader =
+    typename std::conditional<DWORD, RowDma4<ROWS, THREADS>, RowDmaLoader<ROWS, THREADS>>::type;
 template <bool DWORD, bool KM, int MODE, int ROWS, int THREADS>
 using FlatLoader =
     typename std::conditional<DWORD, DmaLoader4<ROWS, THREADS>, Loader<KM, MODE, ROWS, THREADS>>::type;
@@ -747,9 +753,7 @@ __global__ __launch_bounds__(CFG::kThreads, CFG::kMinBlocks) void kernel(const f
   // 4-byte forms. Measured against the 4-byte forms throughout, TFLOP/s:
   // 8192 x 8192 x 8191 139.8 -> 147.9, 4096 x 4096 x 2047 136.2 -> 143.6,
   // 4097 x 2049 x 3001 (edge strips beside) 123.8 -> 128.9.
-  constexpr int kWaves = kThreads / 64;
-  constexpr bool kWhole16 = kDword && (kRowA ? BM * 4 == 1024 : BM % (16 * kWaves) == 0) &&
-                            (kRowB ? BN * 4 == 1024 : BN % (16 * kWaves) == 0);
+  constexpr bool kWhole16 = kDword && (kRowA ? BM % 64 == 0 : BM % 16 == 0) && (kRowB ? BN % 64 == 0 : BN % 16 == 0);
   using LA16 = typename std::conditional<
       kWhole16, typename std::conditional<kRowA, RowDmaLoader<BM, kThreads>, DmaLoader<BM, kThreads, 0>>::type,
       LA>::type;
@@ -1776,11 +1780,13 @@ int mode_of(int64_t m, int64_t n, int64_t k, int64_t bm, int64_t bn, int64_t bk)
   return m % bm == 0 && n % bn == 0 ? 0 : 1;
 }
 
-// Modes 0 and 1 load the k-contiguous operands (A unless TA, B if TB)
-// straight into LDS with 16-byte LDS-DMA, which needs every row of every
-// batch matrix 16-byte aligned. K % 16 == 0 in those modes, so rows inside a
-// matrix follow from its origin: the base pointer and each batch stride must
-// be multiples of 16 bytes. Mode 2's register-staged loads serve the rest.
+// The fp64 kernels' modes 0 and 1 and the narrow fp32 kernel load the
+// k-contiguous operands (A unless TA, B if TB) with 16-byte LDS-DMA under a
+// 16-byte row alignment contract. K % 16 == 0 in those modes, so rows inside
+// a matrix follow from its origin: the base pointer and each batch stride
+// must be multiples of 16 bytes. (The fp32 tiled kernels' 16-byte LDS-DMA
+// runs at any element alignment: the memory path takes 4-byte aligned
+// addresses, as the unaligned-operand tests check.)
 template <typename T, bool TA, bool TB>
 bool dma_aligned(const T* a, const T* b, const BatchDesc& bd) {
   auto aligned = [&](const T* p, const int64_t* strides) {
@@ -1804,10 +1810,9 @@ bool dma_offsets_fit(int64_t k, int64_t lda, int64_t ldb, int64_t bm, int64_t bn
   return fits(a_span) && fits(b_span);
 }
 
-// RowDmaLoader needs every k row of its operand (A if TA, B unless TB)
-// 16-byte aligned: the base pointer and each batch stride, the leading
-// dimension, and the tile origins along the rows (multiples of the tile, or
-// extent - tile for the moved edge tiles of mode 1).
+// The narrow kernel's row LDS-DMA contract: every k row of the K-strided
+// operand (A if TA, B unless TB) 16-byte aligned: the base pointer and each
+// batch stride, the leading dimension, and the tile origins along the rows.
 template <bool TA, bool TB>
 bool rows_aligned(const float* a, const float* b, const BatchDesc& bd, int64_t m, int64_t n, int64_t lda,
                   int64_t ldb) {
@@ -1826,18 +1831,17 @@ void run_f32_config(hp_ctx* ctx, const float* a, const float* b, float* c, int64
                     const BatchDesc& bd, int64_t batch, int64_t lda, int64_t ldb, int64_t ldc) {
   using namespace f32;
   constexpr int BM = CFG::BM, BN = CFG::BN, T = CFG::kThreads;
-  // A K-strided operand (A if TA, B unless TB) goes by row LDS-DMA in modes 0
-  // and 1: the 16-byte form for the 1 KB rows of 256-wide tiles when they are
-  // 16-byte aligned, the 4-byte form for narrower tiles.
+  // A K-strided operand (A if TA, B unless TB) goes by 16-byte row LDS-DMA
+  // in modes 0 and 1; both operands by LDS-DMA in mode 2 when the 32-bit
+  // offsets fit. The 16-byte LDS-DMA needs 4-byte aligned addresses only.
   constexpr bool kRows = TA || !TB;
-  constexpr bool kWide = BM * 4 == 1024 && BN * 4 == 1024;
   TileMap tm;
   prepare(m, n, batch, BM, BN, tm, lda, ldb, ldc);
   auto fix = fixup_kernel<float, hpd::f32x4, Layout<CFG>>;
   int mode = mode_of(m, n, k, BM, BN, BK);
   const bool fits = dma_offsets_fit<TA, TB>(k, lda, ldb, BM, BN);
-  if (!dma_aligned<float, TA, TB>(a, b, bd) || !fits) mode = 2;
-  const bool rows = kRows && mode != 2 && (!kWide || rows_aligned<TA, TB>(a, b, bd, m, n, lda, ldb));
+  if (!fits) mode = 2;
+  const bool rows = kRows && mode != 2;
   auto run = [&](auto whole, auto cut, bool moved) {
     launch_split<float, BM, BN>(ctx, whole, cut, fix, T, a, b, c, m, n, k, bd, tm, BK, "gemm_f32", moved);
   };
