@@ -323,9 +323,24 @@ def bench_extras(p, hip, only, skip_cpu):
 
     timer = Timer(hip)
     extra = {}
+    # CPU legs run after every GPU timing: a BLAS call leaves its threads
+    # spinning for a while, which slowed the launching thread of the next
+    # GPU workload (the compiled MLP: 85% against 90% of peak). Host copies
+    # of the inputs are taken right away, the CPU work is queued here.
+    legs = []
+
+    def later(fn):
+        legs.append(fn)
 
     def want(name):
-        return not only or name in only
+        # Each workload starts from an empty allocation cache: its operands
+        # are then fresh allocations whatever ran before (after the whole
+        # bench had cached ~11 GB of other sizes, the compiled MLP measured
+        # 86-90% of peak from one run to the next, 90% from an empty cache).
+        selected = not only or name in only
+        if selected:
+            hip.release_cached_memory()
+        return selected
 
     def hbm(key, bytes_moved, ms, wall, traffic_key):
         extra[key] = {
@@ -356,17 +371,22 @@ def bench_extras(p, hip, only, skip_cpu):
         if not skip_cpu:
             rows = 4096
             host_a, host_x = p.asnumpy(A[:rows]), p.asnumpy(x)
-            extra["gemv_f32_16384"]["cpu_baseline"] = cpu_blas(
-                lambda: numpy_backend.matmul(host_a, host_x), rows * n * 4 + (rows + n) * 4, "GB/s",
-                f"np.matmul float32 A[:{rows}] @ x (n=16384)")
-            batch = 100  # calls per timing: one call is a few microseconds
-            cores, sec, calls, sec1, calls1 = cpu_blas_seconds(lambda: [numpy_backend.matmul(host_x, host_x) for _ in range(batch)])
-            extra["dot_f32_16384"]["cpu_baseline"] = {
-                "value": round(sec / batch * 1e6, 3), "unit": "us", "cores": cores, "kind": "port",
-                "sample": f"np.matmul(x, x), n=16384; median of {calls} timings of {batch} calls",
-                "one_thread": {"value": round(sec1 / batch * 1e6, 3), "unit": "us", "cores": 1, "calls": calls1},
-            }
-            del host_a
+
+            def gemv_legs(host_a=host_a, host_x=host_x, rows=rows, n=n):
+                extra["gemv_f32_16384"]["cpu_baseline"] = cpu_blas(
+                    lambda: numpy_backend.matmul(host_a, host_x), rows * n * 4 + (rows + n) * 4, "GB/s",
+                    f"np.matmul float32 A[:{rows}] @ x (n=16384)")
+                batch = 100  # calls per timing: one call is a few microseconds
+                cores, sec, calls, sec1, calls1 = cpu_blas_seconds(
+                    lambda: [numpy_backend.matmul(host_x, host_x) for _ in range(batch)])
+                extra["dot_f32_16384"]["cpu_baseline"] = {
+                    "value": round(sec / batch * 1e6, 3), "unit": "us", "cores": cores, "kind": "port",
+                    "sample": f"np.matmul(x, x), n=16384; median of {calls} timings of {batch} calls",
+                    "one_thread": {"value": round(sec1 / batch * 1e6, 3), "unit": "us", "cores": 1, "calls": calls1},
+                }
+
+            later(gemv_legs)
+            del host_a, host_x
         del A
     if want("norm"):
         n = 1 << 28
@@ -381,16 +401,17 @@ def bench_extras(p, hip, only, skip_cpu):
             hbm(key, n * np.dtype(dtype).itemsize, ms, wall, f"norm_{dtype}")
             if not skip_cpu:
                 sample = p.asnumpy(x[: 1 << 22])
-                extra[key]["cpu_baseline"] = cpu_single(
-                    lambda: numpy_backend.norm(sample), sample.nbytes, "GB/s", f"two-pass NumPy norm of 2^22 {dtype}")
+                later(lambda key=key, sample=sample, dtype=dtype: extra[key].__setitem__("cpu_baseline", cpu_single(
+                    lambda: numpy_backend.norm(sample), sample.nbytes, "GB/s", f"two-pass NumPy norm of 2^22 {dtype}")))
             del x
         rows = p.random.default_rng(2, backend=hip).uniform(-1, 1, (65536, 4096), dtype="float32")
         ms, wall = timer.run(lambda: p.linalg.norm(rows, axis=1), 10)
         hbm("norm_rows_f32_65536x4096", 65536 * 4096 * 4 + 65536 * 4, ms, wall, "norm_rows")
         if not skip_cpu:
             sample = p.asnumpy(rows[:1024])
-            extra["norm_rows_f32_65536x4096"]["cpu_baseline"] = cpu_single(
-                lambda: numpy_backend.norm(sample, axis=1), sample.nbytes + 1024 * 4, "GB/s", "two-pass NumPy norm, axis=1, of 1024x4096 float32")
+            later(lambda sample=sample: extra["norm_rows_f32_65536x4096"].__setitem__("cpu_baseline", cpu_single(
+                lambda: numpy_backend.norm(sample, axis=1), sample.nbytes + 1024 * 4, "GB/s",
+                "two-pass NumPy norm, axis=1, of 1024x4096 float32")))
         del rows
     if want("strided"):
         rows, cols = 262144, 1024
@@ -406,9 +427,9 @@ def bench_extras(p, hip, only, skip_cpu):
             key = f"{name}_axis0_f32_262144x1024"
             hbm(key, bytes_moved, ms, wall, f"strided_{name}")
             if sample is not None:
-                extra[key]["cpu_baseline"] = cpu_single(
-                    host_fn, sample.nbytes + cols * 4, "GB/s", f"NumPy {name} over axis 0 of a 16384x1024 float32 sample")
-        del data, sample
+                later(lambda key=key, host_fn=host_fn, name=name, nbytes=sample.nbytes + cols * 4: extra[key].__setitem__(
+                    "cpu_baseline", cpu_single(host_fn, nbytes, "GB/s", f"NumPy {name} over axis 0 of a 16384x1024 float32 sample")))
+        del data
     if want("rng"):
         n = 1 << 28
         for dist in ("uniform", "normal", "exponential"):
@@ -425,9 +446,9 @@ def bench_extras(p, hip, only, skip_cpu):
             }
             if not skip_cpu:
                 count = 1 << 20
-                extra[key]["cpu_baseline"] = cpu_single(
+                later(lambda key=key, dist=dist, count=count: extra[key].__setitem__("cpu_baseline", cpu_single(
                     lambda: numpy_backend.random(dist, "float32", (count,), 42), count, "Gsample/s",
-                    f"NumPy Philox {dist} float32, 2^20 samples")
+                    f"NumPy Philox {dist} float32, 2^20 samples")))
     if want("gemm_f64"):
         n = 4096
         rng = p.random.default_rng(3, backend=hip)
@@ -437,8 +458,8 @@ def bench_extras(p, hip, only, skip_cpu):
         mfma("gemm_f64_4096", 2.0 * n**3, ms, "gemm_f64", bound="mfma_fp64")
         if not skip_cpu:
             ha, hb = p.asnumpy(a[:512]), p.asnumpy(b)
-            extra["gemm_f64_4096"]["cpu_baseline"] = cpu_blas(
-                lambda: numpy_backend.matmul(ha, hb), 2.0 * 512 * n * n, "GFLOP/s", "np.matmul float64 A[:512] @ B (4096x4096)")
+            later(lambda ha=ha, hb=hb, n=n: extra["gemm_f64_4096"].__setitem__("cpu_baseline", cpu_blas(
+                lambda: numpy_backend.matmul(ha, hb), 2.0 * 512 * n * n, "GFLOP/s", "np.matmul float64 A[:512] @ B (4096x4096)")))
         del a, b
     if want("gemm_padded"):
         m, k, n = 4097, 3001, 2049
@@ -452,9 +473,14 @@ def bench_extras(p, hip, only, skip_cpu):
         mfma("gemm_f32_4097x3001x2049_unpadded", flops, ms, "gemm_unpadded")
         if not skip_cpu:
             ha, hb = p.asnumpy(a[:1024]), p.asnumpy(b)
-            leg = cpu_blas(lambda: numpy_backend.matmul(ha, hb), 2.0 * 1024 * n * k, "GFLOP/s", "np.matmul float32 A[:1024] @ B (3001x2049)")
-            extra["gemm_f32_4097x3001x2049_padded"]["cpu_baseline"] = leg
-            extra["gemm_f32_4097x3001x2049_unpadded"]["cpu_baseline"] = leg
+
+            def padded_leg(ha=ha, hb=hb, n=n, k=k):
+                leg = cpu_blas(lambda: numpy_backend.matmul(ha, hb), 2.0 * 1024 * n * k, "GFLOP/s",
+                               "np.matmul float32 A[:1024] @ B (3001x2049)")
+                extra["gemm_f32_4097x3001x2049_padded"]["cpu_baseline"] = leg
+                extra["gemm_f32_4097x3001x2049_unpadded"]["cpu_baseline"] = leg
+
+            later(padded_leg)
         del a, b
     if want("gemm_batched"):
         rng = p.random.default_rng(3, backend=hip)
@@ -464,8 +490,9 @@ def bench_extras(p, hip, only, skip_cpu):
         mfma("gemm_f32_batched_64x512x1024x768", 2.0 * 64 * 512 * 768 * 1024, ms, "gemm_batched")
         if not skip_cpu:
             ha, hb = p.asnumpy(a[:8]), p.asnumpy(b)
-            extra["gemm_f32_batched_64x512x1024x768"]["cpu_baseline"] = cpu_blas(
-                lambda: numpy_backend.matmul(ha, hb), 2.0 * 8 * 512 * 768 * 1024, "GFLOP/s", "np.matmul float32 A[:8] @ B, batch of 8")
+            later(lambda ha=ha, hb=hb: extra["gemm_f32_batched_64x512x1024x768"].__setitem__("cpu_baseline", cpu_blas(
+                lambda: numpy_backend.matmul(ha, hb), 2.0 * 8 * 512 * 768 * 1024, "GFLOP/s",
+                "np.matmul float32 A[:8] @ B, batch of 8")))
         del a, b
     if want("gemm_small"):
         # Config 1's shape: 1024^3 float32, seed 0 host inputs; the GPU product
@@ -481,11 +508,17 @@ def bench_extras(p, hip, only, skip_cpu):
         got = p.asnumpy(a @ b).astype(np.float64)
         extra["gemm_f32_1024"]["rel_l2_vs_float64"] = float(np.linalg.norm(got - exact64) / np.linalg.norm(exact64))
         if not skip_cpu:
-            leg = cpu_blas(lambda: numpy_backend.matmul(ha, hb), flops, "GFLOP/s", "config 1: np.matmul float32 1024x1024x1024, seed 0")
-            cpu_c = numpy_backend.matmul(ha, hb).astype(np.float64)
-            leg["rel_l2_vs_float64"] = float(np.linalg.norm(cpu_c - exact64) / np.linalg.norm(exact64))
-            extra["gemm_f32_1024"]["cpu_baseline"] = leg
-            extra["config1_cpu_gemm_f32_1024"] = dict(leg, note="BASELINE config 1 (the reference NumPy backend path), measured on this host")
+
+            def config1_leg(ha=ha, hb=hb, flops=flops, exact64=exact64):
+                leg = cpu_blas(lambda: numpy_backend.matmul(ha, hb), flops, "GFLOP/s",
+                               "config 1: np.matmul float32 1024x1024x1024, seed 0")
+                cpu_c = numpy_backend.matmul(ha, hb).astype(np.float64)
+                leg["rel_l2_vs_float64"] = float(np.linalg.norm(cpu_c - exact64) / np.linalg.norm(exact64))
+                extra["gemm_f32_1024"]["cpu_baseline"] = leg
+                extra["config1_cpu_gemm_f32_1024"] = dict(
+                    leg, note="BASELINE config 1 (the reference NumPy backend path), measured on this host")
+
+            later(config1_leg)
         del a, b
     if only and "copy" in only:
         # Calibration for rocprofv3 --pmc: a plain 1 GiB float32 copy
@@ -527,10 +560,12 @@ def bench_extras(p, hip, only, skip_cpu):
                     h = np.tanh(numpy_backend.matmul(h, w) + bias)
                 return h.mean(axis=1)
 
-            extra["mlp_forward_f32_8192x4096"]["cpu_baseline"] = cpu_blas(
-                forward, flops * rows / 8192, "GFLOP/s", f"NumPy forward of {rows} rows (np.matmul + np.tanh + mean)")
+            later(lambda work=flops * rows / 8192, rows=rows: extra["mlp_forward_f32_8192x4096"].__setitem__(
+                "cpu_baseline", cpu_blas(forward, work, "GFLOP/s", f"NumPy forward of {rows} rows (np.matmul + np.tanh + mean)")))
     if want("vendor"):
         extra.update(vendor_gemm())
+    for leg in legs:
+        leg()
     return extra
 
 
@@ -560,13 +595,14 @@ def main(argv=None):
     gemm = bench_gemm(p, hip, args.steps, args.warmup)
     gflops = gemm["flops"] / (gemm["wall_ms"] * 1e-3) / 1e9
     log(f"gemm: kernel {gemm['kernel_ms']:.3f} ms, wall {gemm['wall_ms']:.3f} ms, {gflops:.0f} GFLOP/s")
+    only = set() if not args.only else {s.strip() for s in args.only.split(",") if s.strip()}
+    extra = {} if only == {"none"} else bench_extras(p, hip, only, args.skip_cpu)
+    # The CPU legs run after every GPU timing (see bench_extras).
     cpu = None
     if not args.skip_cpu:
         log("cpu baseline: np.matmul row sample")
         cpu = cpu_gemm_baseline(p, gemm)
     del gemm["a"], gemm["b"]
-    only = set() if not args.only else {s.strip() for s in args.only.split(",") if s.strip()}
-    extra = {} if only == {"none"} else bench_extras(p, hip, only, args.skip_cpu)
     vendor = extra.get("vendor_gemm_f32_8192")
     if vendor:
         vendor["hip_over_vendor"] = round(vendor["kernel_ms"] / gemm["kernel_ms"], 4)
