@@ -1749,6 +1749,27 @@ struct SideStream {
   ~SideStream() { ctx->stream = main; }
 };
 
+// Joins the side stream back into the main one when it leaves scope (work
+// queued on the main stream afterwards waits for the side stream's), then
+// frees the side stream's pool temporaries, whose frees are ordered on the
+// main stream. Errors while joining are not thrown from the destructor: a
+// failed event call leaves the HIP error for the next checked call.
+struct SideJoin {
+  hp_ctx* ctx;
+  std::vector<void*> deferred;
+  explicit SideJoin(hp_ctx* c) : ctx(c) {}
+  ~SideJoin() {
+    if (hipEventRecord(ctx->join, ctx->side) != hipSuccess || hipStreamWaitEvent(ctx->stream, ctx->join, 0) != hipSuccess)
+      (void)hipStreamSynchronize(ctx->side);
+    for (void* p : deferred) {
+      try {
+        hp::scratch_free(ctx, p);
+      } catch (...) {
+      }
+    }
+  }
+};
+
 // Launches the whole-tile kernel over the complete rounds and, if tiles are
 // cut, the stream-K kernel and the fixup over a pooled workspace.
 template <typename T, int BM, int BN, typename Whole, typename Cut, typename Fix>
@@ -2006,18 +2027,15 @@ void run_f32(hp_ctx* ctx, const float* a, const float* b, float* c, int64_t m, i
       // tiles little, where run after them they and the launch gaps between
       // them added a tenth to the product. The main stream waits for them
       // before its next work; their pool temporaries are freed after that.
-      std::vector<void*> deferred;
       HP_CHECK(hipEventRecord(ctx->fork, ctx->stream));
       HP_CHECK(hipStreamWaitEvent(ctx->side, ctx->fork, 0));
+      SideJoin join(ctx);  // also on an error part way
       {
         SideStream on_side(ctx);
-        if (split_cols) hpgemm::edge_cols_f32(ctx, a, b + nt * st.bs_n, c + nt, mt, int(cols), k, st, n, &deferred);
-        if (split_rows) hpgemm::edge_rows_f32(ctx, a + mt * st.as_r, b, c + mt * n, int(rows), n, k, st, n, &deferred);
+        if (split_cols) hpgemm::edge_cols_f32(ctx, a, b + nt * st.bs_n, c + nt, mt, int(cols), k, st, n, &join.deferred);
+        if (split_rows) hpgemm::edge_rows_f32(ctx, a + mt * st.as_r, b, c + mt * n, int(rows), n, k, st, n, &join.deferred);
       }
       run_f32_tiles<TA, TB>(ctx, a, b, c, mt, nt, k, bd, 1, lda, ldb, n);
-      HP_CHECK(hipEventRecord(ctx->join, ctx->side));
-      HP_CHECK(hipStreamWaitEvent(ctx->stream, ctx->join, 0));
-      for (void* p : deferred) hp::scratch_free(ctx, p);
       return;
     }
   }
