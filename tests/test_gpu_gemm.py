@@ -411,11 +411,14 @@ WIDE_CASES = [
 ]
 
 
-@pytest.mark.parametrize("ta,tb", [(False, False), (True, False), (False, True), (True, True)])
-@pytest.mark.parametrize("batch,m,n,k", WIDE_CASES)
+LAYOUTS = [(False, False), (True, False), (False, True), (True, True)]
+
+
+@pytest.mark.parametrize(
+    "ta,tb,batch,m,n,k",
+    [(ta, tb) + case for case in WIDE_CASES for ta, tb in LAYOUTS if not (case[0] and (ta or tb))],
+)  # transposed operands are 2-D
 def test_wide_tiles_against_float64_and_deterministic(hip, ta, tb, batch, m, n, k):
-    if batch and (ta or tb):
-        pytest.skip("transposed operands are 2-D")
     rng = np.random.default_rng(3 * m + n + 13 * k + 2 * ta + tb)
     left = rng.uniform(-1, 1, batch + ((k, m) if ta else (m, k))).astype(np.float32)
     right = rng.uniform(-1, 1, (n, k) if tb else (k, n)).astype(np.float32)
@@ -444,7 +447,7 @@ def test_wide_tiles_against_float64_and_deterministic(hip, ta, tb, batch, m, n, 
 ODD_K_CASES = [(4096, 4096, 161), (1024, 1024, 4097), (520, 300, 2049)]
 
 
-@pytest.mark.parametrize("ta,tb", [(False, False), (True, False), (False, True), (True, True)])
+@pytest.mark.parametrize("ta,tb", LAYOUTS)
 @pytest.mark.parametrize("m,n,k", ODD_K_CASES)
 def test_odd_k_products_against_float64_and_deterministic(hip, ta, tb, m, n, k):
     rng = np.random.default_rng(m + 7 * n + 3 * k + 2 * ta + tb)
