@@ -13,6 +13,7 @@ Prints ONE JSON line on stdout; progress goes to stderr.
 
 import argparse
 import ctypes
+import gc
 import json
 import os
 import statistics
@@ -66,12 +67,19 @@ class Timer:
     def run(self, fn, reps, warmup=2):
         lib, ctx = self.backend._lib, self.backend._ctx
         warm(fn, self.backend.synchronize, warmup)
-        wall0 = time.perf_counter()
-        lib.hp_event_record(ctx, self.start)
-        for _ in range(reps):
-            fn()
-        lib.hp_event_record(ctx, self.stop)
-        self.backend.synchronize()
+        # As timeit does: no garbage-collection pass inside the timed region
+        # (a pass while the stream is empty shows up as device idle time).
+        gc.collect()
+        gc.disable()
+        try:
+            wall0 = time.perf_counter()
+            lib.hp_event_record(ctx, self.start)
+            for _ in range(reps):
+                fn()
+            lib.hp_event_record(ctx, self.stop)
+            self.backend.synchronize()
+        finally:
+            gc.enable()
         wall = (time.perf_counter() - wall0) * 1e3 / reps
         ms = ctypes.c_float()
         assert lib.hp_event_elapsed_ms(self.start, self.stop, ctypes.byref(ms)) == 0
@@ -213,13 +221,18 @@ def bench_gemm(p, hip, steps, warmup):
     for _ in range(warmup):
         a @ b
     hip.synchronize()
-    wall0 = time.perf_counter()
-    lib, ctx = hip._lib, hip._ctx
-    lib.hp_event_record(ctx, timer.start)
-    for _ in range(steps):
-        c = a @ b
-    lib.hp_event_record(ctx, timer.stop)
-    hip.synchronize()
+    gc.collect()
+    gc.disable()
+    try:
+        wall0 = time.perf_counter()
+        lib, ctx = hip._lib, hip._ctx
+        lib.hp_event_record(ctx, timer.start)
+        for _ in range(steps):
+            c = a @ b
+        lib.hp_event_record(ctx, timer.stop)
+        hip.synchronize()
+    finally:
+        gc.enable()
     wall_ms = (time.perf_counter() - wall0) * 1e3 / steps
     ms = ctypes.c_float()
     lib.hp_event_elapsed_ms(timer.start, timer.stop, ctypes.byref(ms))
