@@ -664,6 +664,36 @@ EDGE_CASES = [
 ]
 
 
+def test_edge_strips_are_ordered_before_the_next_work_on_the_stream(hip):
+    """The strips of a 4097 x 2049 x 1025 product (one edge row, one edge
+    column) run on the context's second stream; the next calls on the main
+    stream, queued without a host wait, must see their outputs (a copy of C)
+    and must not overwrite their inputs before they have read them (a fill
+    of A). C starts as NaN, so a strip output read too early shows."""
+    m, k, n = 4097, 2049, 1025
+    rng = np.random.default_rng(11)
+    a = rng.uniform(-1, 1, (m, k)).astype(np.float32)
+    b = rng.uniform(-1, 1, (k, n)).astype(np.float32)
+    want = a.astype(np.float64) @ b.astype(np.float64)
+    scale = np.abs(a).astype(np.float64) @ np.abs(b).astype(np.float64)
+    bound = 4e-7 * np.sqrt(k) * 4
+    A, B = hip.upload(a.ravel()), hip.upload(b.ravel())
+    C, D = hip.upload(np.zeros(m * n, np.float32)), hip.upload(np.zeros(m * n, np.float32))
+    nan_bits = int(np.array(np.nan, np.float32).view(np.uint32))
+    with hip._active():
+        for _ in range(3):
+            hip._call("hp_h2d", ctypes.c_void_p(A.ptr), ctypes.c_void_p(a.ctypes.data), a.nbytes)
+            hip._call("hp_fill", ctypes.c_void_p(C.ptr), m * n, 4, ctypes.c_uint64(nan_bits))
+            hip._call("hp_gemm", 5, ctypes.c_void_p(A.ptr), ctypes.c_void_p(B.ptr), ctypes.c_void_p(C.ptr), m, n, k,
+                      0, None, None, None)
+            hip._call("hp_d2d", ctypes.c_void_p(D.ptr), ctypes.c_void_p(C.ptr), m * n * 4)
+            hip._call("hp_fill", ctypes.c_void_p(A.ptr), m * k, 4, ctypes.c_uint64(0))
+            got = np.empty(m * n, np.float32)
+            hip._call("hp_d2h", ctypes.c_void_p(got.ctypes.data), ctypes.c_void_p(D.ptr), got.nbytes)
+            got = got.reshape(m, n).astype(np.float64)
+            assert np.all(np.abs(got - want) <= bound * scale + 1e-30)
+
+
 @pytest.mark.parametrize("m,k,n", EDGE_CASES)
 def test_edge_strips_against_float64_and_repeatable(hip, m, k, n):
     rng = np.random.default_rng(m * 5 + k + n)
