@@ -408,6 +408,8 @@ WIDE_CASES = [
     ((), 4000, 2900, 333),  # M, N and K edges
     ((2,), 2048, 3072, 160),  # batched
     ((), 2048, 6000, 64),  # short K, N edge of 48 columns
+    ((240,), 100, 100, 50),  # matrices smaller than a tile: every slice by 4-byte DMA
+    ((14,), 4096, 150, 64),  # N below the tile width
 ]
 
 
