@@ -350,8 +350,9 @@ def bench_extras(p, hip, only, skip_cpu):
     def later(fn):
         legs.append(fn)
 
-    def want(name):
-        # Each workload starts from an empty allocation cache: its operands
+    def begin(name):
+        # Whether workload `name` is selected; a selected workload starts
+        # from an empty allocation cache: its operands
         # are then fresh allocations whatever ran before (after the whole
         # bench had cached ~11 GB of other sizes, the compiled MLP measured
         # 86-90% of peak from one run to the next, 90% from an empty cache).
@@ -377,7 +378,7 @@ def bench_extras(p, hip, only, skip_cpu):
             "roofline": roofline(bound, flops, ms, _traffic(traffic_key)),
         }
 
-    if want("gemv"):
+    if begin("gemv"):
         n = 16384
         rng = p.random.default_rng(1, backend=hip)
         A = rng.uniform(-1, 1, (n, n), dtype="float32")
@@ -406,7 +407,7 @@ def bench_extras(p, hip, only, skip_cpu):
             later(gemv_legs)
             del host_a, host_x
         del A
-    if want("norm"):
+    if begin("norm"):
         n = 1 << 28
         for dtype, decades in (("float32", 30.0), ("float64", 300.0)):
             rng = p.random.default_rng(2, backend=hip)
@@ -431,7 +432,7 @@ def bench_extras(p, hip, only, skip_cpu):
                 lambda: numpy_backend.norm(sample, axis=1), sample.nbytes + 1024 * 4, "GB/s",
                 "two-pass NumPy norm, axis=1, of 1024x4096 float32")))
         del rows
-    if want("strided"):
+    if begin("strided"):
         rows, cols = 262144, 1024
         data = p.random.default_rng(3, backend=hip).uniform(-1, 1, (rows, cols), dtype="float32")
         bytes_moved = rows * cols * 4 + cols * 4
@@ -448,7 +449,7 @@ def bench_extras(p, hip, only, skip_cpu):
                 later(lambda key=key, host_fn=host_fn, name=name, nbytes=sample.nbytes + cols * 4: extra[key].__setitem__(
                     "cpu_baseline", cpu_single(host_fn, nbytes, "GB/s", f"NumPy {name} over axis 0 of a 16384x1024 float32 sample")))
         del data
-    if want("rng"):
+    if begin("rng"):
         n = 1 << 28
         for dist in ("uniform", "normal", "exponential"):
             rng = p.random.default_rng(42, backend=hip)
@@ -467,7 +468,7 @@ def bench_extras(p, hip, only, skip_cpu):
                 later(lambda key=key, dist=dist, count=count: extra[key].__setitem__("cpu_baseline", cpu_single(
                     lambda: numpy_backend.random(dist, "float32", (count,), 42), count, "Gsample/s",
                     f"NumPy Philox {dist} float32, 2^20 samples")))
-    if want("gemm_f64"):
+    if begin("gemm_f64"):
         n = 4096
         rng = p.random.default_rng(3, backend=hip)
         a = rng.uniform(-1, 1, (n, n), dtype="float64")
@@ -479,7 +480,7 @@ def bench_extras(p, hip, only, skip_cpu):
             later(lambda ha=ha, hb=hb, n=n: extra["gemm_f64_4096"].__setitem__("cpu_baseline", cpu_blas(
                 lambda: numpy_backend.matmul(ha, hb), 2.0 * 512 * n * n, "GFLOP/s", "np.matmul float64 A[:512] @ B (4096x4096)")))
         del a, b
-    if want("gemm_padded"):
+    if begin("gemm_padded"):
         m, k, n = 4097, 3001, 2049
         rng = p.random.default_rng(3, backend=hip)
         a = rng.uniform(-1, 1, (m, k), dtype="float32")
@@ -500,7 +501,7 @@ def bench_extras(p, hip, only, skip_cpu):
 
             later(padded_leg)
         del a, b
-    if want("gemm_batched"):
+    if begin("gemm_batched"):
         rng = p.random.default_rng(3, backend=hip)
         a = rng.uniform(-1, 1, (64, 512, 1024), dtype="float32")
         b = rng.uniform(-1, 1, (1024, 768), dtype="float32")
@@ -512,7 +513,7 @@ def bench_extras(p, hip, only, skip_cpu):
                 lambda: numpy_backend.matmul(ha, hb), 2.0 * 8 * 512 * 768 * 1024, "GFLOP/s",
                 "np.matmul float32 A[:8] @ B, batch of 8")))
         del a, b
-    if want("gemm_small"):
+    if begin("gemm_small"):
         # Config 1's shape: 1024^3 float32, seed 0 host inputs; the GPU product
         # beside the reference CPU path itself (NumPy's BLAS) and its error.
         gen = np.random.default_rng(0)
@@ -546,7 +547,7 @@ def bench_extras(p, hip, only, skip_cpu):
         ms, wall = timer.run(lambda: src.copy(), 5)
         extra["copy_f32_2^28"] = {"value": round(2 * n * 4 / (ms * 1e-3) / 1e9, 1), "unit": "GB/s", "kernel_us": round(ms * 1e3, 2)}
         del src
-    if want("mlp"):
+    if begin("mlp"):
         rng = p.random.default_rng(42, backend=hip)
         widths = (4096, 4096, 4096, 1024)
         params = []
@@ -580,7 +581,7 @@ def bench_extras(p, hip, only, skip_cpu):
 
             later(lambda work=flops * rows / 8192, rows=rows: extra["mlp_forward_f32_8192x4096"].__setitem__(
                 "cpu_baseline", cpu_blas(forward, work, "GFLOP/s", f"NumPy forward of {rows} rows (np.matmul + np.tanh + mean)")))
-    if want("vendor"):
+    if begin("vendor"):
         extra.update(vendor_gemm())
     for leg in legs:
         leg()
