@@ -573,10 +573,15 @@ struct DmaLoader4 {
   // Element (r, k) of the tile at p[(r0 + r) * ld + k], valid for r0 + r <
   // rows and k < kp; byte offsets from the tile's first row below 2^31 (host
   // check).
-  // Descriptor from the tile's first row through the last valid element.
+  // Descriptor from the tile's first row through the last valid element of
+  // the tile's own rows: (ROWS - 1) * ld + kp elements at most, which the
+  // host's span check keeps below 2^31 bytes. A range through the end of the
+  // whole operand would wrap its 32 bits for operands of 2^29 floats or
+  // more and could exceed kOutOfRange, which must stay outside every range.
   __device__ __forceinline__ static __amdgpu_buffer_rsrc_t rsrc_of(const float* p, int64_t r0, int64_t rows,
                                                                    int64_t ld, int64_t kp) {
-    const int64_t extent = (rows - 1 - r0) * ld + kp;
+    const int64_t own = rows - r0 < ROWS ? rows - r0 : ROWS;
+    const int64_t extent = (own - 1) * ld + kp;
     return __builtin_amdgcn_make_buffer_rsrc(const_cast<float*>(p + r0 * ld), 0, int(4 * extent), 0x00020000);
   }
   __device__ __forceinline__ void issue(const float* p, int64_t r0, int64_t rows, int64_t ld, int64_t kp, int64_t k0,

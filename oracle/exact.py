@@ -6,6 +6,9 @@
   (exact dyadic sums), re-derived here with Python integers.
 - float64_matmul_rows: fp64 recomputation from the rounded fp32 inputs (the
   "higher precision" oracle of reference benchmarks/numerical_metrics.py:45-96).
+- product_bound_ratio: the same recomputation over every output of a 2-D
+  product in row blocks, against the elementwise forward-error bound of a
+  K-term sum (used for full-output checks of config-size products).
 - norm_extended: the Euclidean norm in x86 80-bit long double with two-pass
   power-of-two scaling (64-bit significand, exponent range covers squares of
   1e+-300), used for full-size fp64 norms.
@@ -51,6 +54,33 @@ def relative_error(value, exact):
 def float64_matmul_rows(a, b, rows):
     """float64 product rows a[rows] @ b from the rounded inputs."""
     return np.asarray(a[rows], dtype=np.float64) @ np.asarray(b, dtype=np.float64)
+
+
+def product_bound_ratio(a, b, got, unit, block=1024):
+    """Largest |got - a @ b| / (unit * sqrt(k) * 4 * (|a| @ |b|)) over EVERY
+    output of a 2-D product, with a @ b and |a| @ |b| in float64 from the
+    rounded inputs, computed in row blocks of `block` (8192^3 needs two
+    float64 products, not a float64 copy of C). A value <= 1 means every
+    output lies within the elementwise forward-error bound of a K-term sum in
+    the working precision (unit = 4e-7 for float32, 8e-16 for float64); an
+    output that is NaN, infinite or wrong by O(1) gives inf or >> 1.
+    """
+    a = np.asarray(a)
+    b64 = np.asarray(b, dtype=np.float64)
+    babs = np.abs(b64)
+    got = np.asarray(got)
+    k = a.shape[1]
+    worst = 0.0
+    for r0 in range(0, a.shape[0], block):
+        rows = np.asarray(a[r0 : r0 + block], dtype=np.float64)
+        want = rows @ b64
+        scale = np.abs(rows) @ babs
+        bound = unit * math.sqrt(k) * 4 * scale + 1e-30
+        err = np.abs(np.asarray(got[r0 : r0 + block], dtype=np.float64) - want)
+        if not np.all(np.isfinite(err)):
+            return math.inf
+        worst = max(worst, float(np.max(err / bound)) if err.size else 0.0)
+    return worst
 
 
 def norm_extended(x, axis=None):

@@ -9,8 +9,10 @@ tanh(h @ w + b) per layer and a row-wise mean.
 Checked here:
 - the plan's step kinds equal the reference compiler's golden list;
 - each layer's product (the same hp_gemm launch the plan's matmul step makes)
-  is within 2x the reference custom kernel's error (sequential K, separate
-  rounding) against the exact dyadic oracle on sampled outputs;
+  has every output within the elementwise float32 error bound of a K-term
+  sum against float64, repeats bit for bit, and is within 2x the reference
+  custom kernel's error (sequential K, separate rounding) against the exact
+  dyadic oracle on sampled outputs;
 - the compiled plan's output rows are within 2x the error of the reference
   kernel chain (sequential-K products, float32 tanh, the reference reduce
   order for the mean) against a float64 recomputation from the same weights.
@@ -88,6 +90,9 @@ def test_config5_compiled_mlp_full_size(hip):
     for index, (w_dev, b_dev) in enumerate(zip(params[0::2], params[1::2])):
         product = layer_input @ w_dev
         host_in, host_product = p.asnumpy(layer_input), p.asnumpy(product)
+        # Every output of the layer's whole-tile product, and a bitwise repeat.
+        assert exact.product_bound_ratio(host_in, weights[index], host_product, 4e-7) <= 1, f"layer {index}"
+        np.testing.assert_array_equal(p.asnumpy(layer_input @ w_dev), host_product)
         hip_err, ref_err = _sampled_layer_errors(host_in, weights[index], host_product, 24, 50 + index)
         assert hip_err <= 2 * ref_err, f"layer {index}: {hip_err} > 2 x {ref_err}"
         layer_input = p.tanh(product + b_dev)

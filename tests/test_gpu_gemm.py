@@ -1,4 +1,4 @@
-"""GPU parity of the MFMA GEMM (hp_gemm, hp_pad_copy) against fp64/exact oracles.
+"""GPU parity of the MFMA GEMM (hp_gemm) against fp64/exact oracles.
 
 Cases follow reference tests/test_cuda.py:280-441 (vector/irregular/empty/K=0
 products, NaN/Inf-poisoned destinations, batched broadcasting),
@@ -119,6 +119,7 @@ def test_batched_broadcast_products(hip, dtype, shapes):
         (777, 300, 64),  # moved edge tiles that own 9 rows / 44 columns
         (257, 257, 32),  # moved edge tiles that own a single row / column
         (513, 1023, 16),  # one K slice; edges of 1 row and 255 columns
+        (4096, 4096, 1024),  # whole rounds of interior tiles, no stream-K
     ],
 )
 def test_kernel_modes_against_float64(hip, dtype, m, n, k):
@@ -227,13 +228,15 @@ def test_config4_fp32_8192_cubed(hip):
     rng = np.random.default_rng(3)
     a = rng.uniform(-1, 1, (n, n)).astype(np.float32)
     b = rng.uniform(-1, 1, (n, n)).astype(np.float32)
-    c = p.asarray(a, backend=hip) @ p.asarray(b, backend=hip)
-    rows = np.array([0, 1, 4095, 8191])
+    A, B = p.asarray(a, backend=hip), p.asarray(b, backend=hip)
+    c = A @ B
     got_rows = p.asnumpy(c[4095:4096])  # gather of one row
     assert got_rows.shape == (1, n)
     full = p.asnumpy(c)
-    want = exact.float64_matmul_rows(a, b, rows)
-    np.testing.assert_allclose(full[rows], want, rtol=0, atol=5e-4)
+    # Every output (the whole-tile kernel of the headline: a wrong fragment
+    # block in any tile fails), then the product repeated bit for bit.
+    assert exact.product_bound_ratio(a, b, full, 4e-7) <= 1
+    np.testing.assert_array_equal(p.asnumpy(A @ B), full)
     np.testing.assert_array_equal(full[4095], got_rows[0])
     hip_err, ref_err = _sampled_error_ratio(a, b, full, 48, 6)
     assert hip_err <= 2 * ref_err
@@ -244,7 +247,10 @@ def test_config4_fp64_4096_cubed(hip):
     rng = np.random.default_rng(3)
     a = rng.uniform(-1, 1, (n, n))
     b = rng.uniform(-1, 1, (n, n))
-    full = p.asnumpy(p.asarray(a, backend=hip) @ p.asarray(b, backend=hip))
+    A, B = p.asarray(a, backend=hip), p.asarray(b, backend=hip)
+    full = p.asnumpy(A @ B)
+    assert exact.product_bound_ratio(a, b, full, 8e-16) <= 1
+    np.testing.assert_array_equal(p.asnumpy(A @ B), full)
     hip_err, ref_err = _sampled_error_ratio(a, b, full, 48, 7)
     assert hip_err <= 2 * ref_err
     np.testing.assert_allclose(full[[0, 2047, 4095]], a[[0, 2047, 4095]] @ b, rtol=0, atol=1e-11)
@@ -266,13 +272,18 @@ def test_config4_padded_odd_shape(hip):
     assert info["padded_output_shape"] == expected["padded_output_shape"]
     assert expected["scratch_bytes"] == 109_039_616 and info["scratch_bytes"] == 0
     assert info["copy_dispatches"] == 0 and info["alignment"] == (32, 16, 32)
+    first = None
     for result in (p.matmul(A, B, padding=True), compiled(A, B)):
         got = p.asnumpy(result)
         assert got.shape == (m, n)
-        rows = np.array([0, 2048, 4096])
-        np.testing.assert_allclose(got[rows], exact.float64_matmul_rows(a, b, rows), rtol=0, atol=5e-4)
+        if first is None:
+            first = got
+            assert exact.product_bound_ratio(a, b, got, 4e-7) <= 1  # every output
+        else:
+            np.testing.assert_array_equal(got, first)  # eager and compiled, bit for bit
         hip_err, ref_err = _sampled_error_ratio(a, b, got, 32, 8)
         assert hip_err <= 2 * ref_err
+    np.testing.assert_array_equal(p.asnumpy(A @ B), first)  # the unpadded product too
     np.testing.assert_array_equal(p.asnumpy(A), a)
 
 
@@ -722,3 +733,42 @@ def test_edge_strips_against_float64_and_repeatable(hip, m, k, n):
         hip_strip = np.sqrt(np.mean(((got[rr, cc] - truth) / mag) ** 2))
         ref_strip = np.sqrt(np.mean(((ref - truth) / mag) ** 2))
         assert hip_strip <= 2 * ref_strip + 2.0**-24
+
+
+def _tile_rows_ratio(A, C, b, r0, r1):
+    """Bound ratio of C[r0:r1] against float64 from A's rows (device gathers)."""
+    return exact.product_bound_ratio(p.asnumpy(A[r0:r1]), b, p.asnumpy(C[r0:r1]), 4e-7)
+
+
+def test_k_contiguous_operand_over_4_gib(hip):
+    """Odd K with A of 4.4 GB: the 4-byte LDS-DMA descriptor of a tile spans
+    that tile's own rows. A range through the end of the operand wrapped its
+    32 bits here: the tile at row 7936 saw 1.83 MB of its 4.2 MB and loaded
+    the rest as zeros."""
+    m, k, n = 270000, 4099, 256
+    rng = p.random.default_rng(17, backend=hip)
+    A = rng.uniform(-1, 1, (m, k), dtype="float32")
+    b = np.random.default_rng(18).uniform(-1, 1, (k, n)).astype(np.float32)
+    C = A @ p.asarray(b, backend=hip)
+    for r0 in (0, 7936, 8192, 134912, 269824):
+        ratio = _tile_rows_ratio(A, C, b, r0, min(r0 + 256, m))
+        assert ratio <= 1, f"rows from {r0}: {ratio}"
+
+
+def test_k_edge_lanes_of_a_2_to_4_gib_operand_read_zero(hip):
+    """Odd K with A of 2.46 GB whose rows from 131072 on are +inf. The lanes
+    past K in the K-edge slice take an offset of 2^31 bytes that must lie
+    outside the descriptor's range; with a range above 2^31 they read rows
+    about 131000 further on (inf, times the +0 of B past K: NaN outputs)."""
+    m, k, n = 150000, 4099, 256
+    rng = p.random.default_rng(19, backend=hip)
+    A = rng.uniform(-1, 1, (m, k), dtype="float32")
+    first_inf = 131072
+    with hip._active():
+        hip._call("hp_fill", ctypes.c_void_p(A._data.ptr + first_inf * k * 4), (m - first_inf) * k, 4, 0x7F800000)
+    b = np.random.default_rng(20).uniform(-1, 1, (k, n)).astype(np.float32)
+    C = A @ p.asarray(b, backend=hip)
+    for r0 in (0, 256, 4096, 16384, first_inf - 256):
+        ratio = _tile_rows_ratio(A, C, b, r0, r0 + 256)
+        assert ratio <= 1, f"rows from {r0}: {ratio}"
+    assert not np.isfinite(p.asnumpy(C[first_inf : first_inf + 4])).any()

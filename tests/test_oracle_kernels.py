@@ -41,6 +41,28 @@ def test_exact_norm_known_values_and_fsum_agreement():
     assert exact.norm_exact(x) == pytest.approx(fsum, rel=2e-16)
 
 
+def test_product_bound_ratio_accepts_float_sums_and_rejects_planted_mistakes():
+    rng = np.random.default_rng(12)
+    for dtype, unit in ((np.float32, 4e-7), (np.float64, 8e-16)):
+        a = rng.uniform(-1, 1, (37, 300)).astype(dtype)
+        b = rng.uniform(-1, 1, (300, 23)).astype(dtype)
+        # The sequential working-precision loop (the reference kernel's order)
+        # and the working-precision BLAS product lie inside the bound.
+        assert exact.product_bound_ratio(a, b, kernels.gemm_sequential_rows(a, b), unit, block=8) <= 1
+        assert exact.product_bound_ratio(a, b, a @ b, unit, block=5) <= 1
+        good = (a.astype(np.float64) @ b.astype(np.float64)).astype(dtype)
+        # One output off in its last few bits of float32 stays inside; one
+        # dropped term, a transposed operand or a NaN falls out.
+        dropped = good.copy()
+        dropped[36, 22] -= a[36, 299] * b[299, 22]
+        assert exact.product_bound_ratio(a, b, dropped, unit, block=8) > 1
+        square = rng.uniform(-1, 1, (40, 40)).astype(dtype)
+        assert exact.product_bound_ratio(square, square, square.T @ square, unit) > 1
+        poisoned = good.copy()
+        poisoned[0, 0] = np.nan
+        assert exact.product_bound_ratio(a, b, poisoned, unit) == math.inf
+
+
 def test_extended_norm_matches_exact_on_extreme_inputs():
     rng = np.random.default_rng(11)
     x = 10.0 ** rng.uniform(-300, 300, 2000) * (rng.integers(0, 2, 2000) * 2 - 1)
