@@ -102,12 +102,12 @@ def test_config3_flat_norm_full_size(hip, dtype, decades, n):
     got = float(p.linalg.norm(p.asarray(x, backend=hip)).item())
     oracle = float(exact.norm_extended(x))
     hip_error = abs(got - oracle) / oracle
-    # Reference pair-merge kernel error measured on a 2^22 prefix (same distribution).
-    prefix = x[: 1 << 22]
-    ref_oracle = float(exact.norm_extended(prefix))
-    ref_error = abs(float(kernels.norm_pair_merge(prefix)) - ref_oracle) / ref_oracle
-    prefix_hip = float(p.linalg.norm(p.asarray(prefix, backend=hip)).item())
-    assert abs(prefix_hip - ref_oracle) / ref_oracle <= max(2 * ref_error, np.finfo(dtype).eps)
+    # The reference pair-merge kernel's error on the same full vector (its
+    # three passes over 65,536 chunk pairs, then 16, then 1), with one ulp
+    # of the output as the floor: both results are rounded to dtype, and a
+    # correctly rounded value is already up to half an ulp off.
+    ref_error = abs(float(kernels.norm_pair_merge(x)) - oracle) / oracle
+    assert hip_error <= max(2 * ref_error, np.finfo(dtype).eps), f"{hip_error} > 2 x {ref_error}"
     assert hip_error < 8 * np.finfo(dtype).eps
 
 
