@@ -110,29 +110,58 @@ def _stand_in(trace, name, position, value, static_argnames):
     )
 
 
-def capture_call(function, args, kwargs, *, elementwise_only=False, static_argnames=(), padding=False):
-    """Trace ``function`` once and return ``(plan, bindings)``."""
-    bound = _bind(function, args, kwargs)
-    bindings = tuple(bound.arguments.values())
-    arrays = [v for v in bindings if isinstance(v, ndarray)]
-    if not arrays:
+def _trace_target(values):
+    """The backend that every array argument lives on: the trace's target.
+
+    Refuses a call without arrays, a capture inside a running capture (the
+    arrays would be the outer trace's stand-ins) and arrays of two backends.
+    """
+    homes = [value._backend for value in values if isinstance(value, ndarray)]
+    if not homes:
         raise TypeError("Capture requires at least one OpenPacho array argument")
-    target = arrays[0]._backend
-    if getattr(target, "_is_tracing", False):
+    if getattr(homes[0], "_is_tracing", False):
         raise TypeError("Nested compile/fuse calls are not supported; wrap the outer plain function")
-    if any(v._backend is not target for v in arrays):
+    if len({id(home) for home in homes}) > 1:
         raise BackendMismatchError("Captured arguments belong to different backends/devices")
-    trace = TraceBackend(target, elementwise_only=elementwise_only)
-    for position, name in enumerate(tuple(bound.arguments)):
-        bound.arguments[name] = _stand_in(trace, name, position, bound.arguments[name], static_argnames)
-    with use_backend(trace):
-        result = function(*bound.args, **bound.kwargs)
+    return homes[0]
+
+
+def _plan_outputs(result, elementwise_only):
+    """(outputs, multiple): a tuple result names several outputs, anything
+    else one; every output must be a traced array expression, and fuse()
+    plans have exactly one."""
     multiple = isinstance(result, tuple)
     outputs = result if multiple else (result,)
-    if not outputs or not all(isinstance(v, Expression) for v in outputs):
+    if not outputs or not all(isinstance(value, Expression) for value in outputs):
         raise TypeError("Captured functions must return array expressions")
     if elementwise_only and multiple:
         raise TypeError("fuse must return one elementwise array expression")
+    return outputs, multiple
+
+
+def capture_call(function, args, kwargs, *, elementwise_only=False, static_argnames=(), padding=False):
+    """Run ``function`` once on stand-ins of its arguments and return
+    ``(plan, bindings)``: the plan of the expression graph it built on a
+    recording backend, and the bound argument values (defaults applied) in
+    parameter order, which the plan's InputRef/argument positions index.
+
+    Capture contract (reference _compiler.py:30-68): arrays become
+    expressions of their shape and dtype, numeric scalars become scalar
+    arguments, names in ``static_argnames`` keep their values (they may shape
+    the graph), and anything else is refused.
+    """
+    bound = _bind(function, args, kwargs)
+    bindings = tuple(bound.arguments.values())
+    target = _trace_target(bindings)
+    trace = TraceBackend(target, elementwise_only=elementwise_only)
+    stand_ins = {
+        name: _stand_in(trace, name, position, value, static_argnames)
+        for position, (name, value) in enumerate(bound.arguments.items())
+    }
+    call = inspect.BoundArguments(bound.signature, stand_ins)
+    with use_backend(trace):
+        result = function(*call.args, **call.kwargs)
+    outputs, multiple = _plan_outputs(result, elementwise_only)
     return ExecutionPlan(target, outputs, multiple, padding=padding), bindings
 
 

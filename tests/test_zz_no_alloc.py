@@ -8,6 +8,9 @@ whose temporaries exceed the static workspace must fail before any launch.
 """
 
 import ctypes
+import math
+import re
+from pathlib import Path
 
 import numpy as np
 import pytest
@@ -17,7 +20,9 @@ from openpacho import _hip_lib
 
 pytestmark = pytest.mark.gpu
 
-SCRATCH_BYTES = 4 << 20
+HEADER = Path(__file__).resolve().parents[1] / "include" / "pacho_hip.h"
+_DEFINE = re.search(r"#define HP_NORM_NOALLOC_SCRATCH_BYTES \((\d+) << (\d+)\)", HEADER.read_text())
+SCRATCH_BYTES = int(_DEFINE.group(1)) << int(_DEFINE.group(2))
 
 # (dtype, outer, reduced, inner): the first of each pair is the larger call.
 CASES = [
@@ -31,6 +36,9 @@ CASES = [
     # one chunk per row (no workspace), strided axis, empty reduced axis
     (np.float32, [(4096, 4096, 1), (17, 100, 1)]),
     (np.float32, [(64, 300, 129), (3, 7, 5)]),
+    # strided axis over three passes: the first pass's pairs in the first
+    # half of the workspace, the second pass's in the half after it
+    (np.float32, [(1, 32768, 1024), (2, 20000, 640)]),
     (np.float64, [(5, 0, 3), (2, 0, 1)]),
 ]
 
@@ -76,9 +84,36 @@ def test_noalloc_matches_hp_norm_on_two_calls(hip, dtype, calls):
             np.testing.assert_allclose(got, ref.ravel(), rtol=2e-6, atol=0)
 
 
+def test_noalloc_workspace_boundary(hip):
+    """Rows of 2049 doubles are two chunks of pairs: 32 bytes of workspace per
+    row and no second merge buffer. SCRATCH_BYTES / 32 rows fill the static
+    array exactly and run; one row more needs 256 bytes beyond it (the pair
+    buffer is rounded up to 256 bytes) and is rejected on the host from the
+    extents alone, before any launch and without touching the pool."""
+    reduced = 2049
+    rows = SCRATCH_BYTES // 32
+    x = p.empty((rows * reduced,), dtype=np.float64, backend=hip)
+    with hip._active():
+        hip._call("hp_fill", ctypes.c_void_p(x._data.ptr), rows * reduced, 8, 0x3FF0000000000000)  # 1.0
+        want = _norms(hip, "hp_norm", x, (rows, reduced, 1), np.float64)
+        out = p.empty((rows,), dtype=np.float64, backend=hip)
+        hip.synchronize()
+        before = _pool(hip)
+        hip._call("hp_norm_noalloc", 6, *hip._ptrs(x, out), rows, reduced, 1)
+        hip.synchronize()
+        assert _pool(hip) == before
+        with pytest.raises(ValueError, match="static scratch"):
+            hip._call("hp_norm_noalloc", 6, *hip._ptrs(x, out), rows + 1, reduced, 1)
+        assert _pool(hip) == before
+    got = p.asnumpy(out)
+    np.testing.assert_array_equal(got.view(np.uint64), p.asnumpy(want).view(np.uint64))
+    assert np.all(got == math.sqrt(reduced))
+
+
 def test_noalloc_rejects_shapes_beyond_the_static_workspace(hip):
-    # 3 rows x 2^19 chunks of 2048 doubles: 16 MiB of pairs. Rejected on the
+    # 3 rows x 2^19 chunks of 2048 doubles: 24 MiB of pairs. Rejected on the
     # host from the extents alone; the pointers are never dereferenced.
+    assert 3 * (1 << 19) * 16 > SCRATCH_BYTES
     x = p.empty((8,), dtype=np.float64, backend=hip)
     out = p.empty((3,), dtype=np.float64, backend=hip)
     with hip._active():
@@ -86,4 +121,3 @@ def test_noalloc_rejects_shapes_beyond_the_static_workspace(hip):
         with pytest.raises(ValueError, match="static scratch"):
             hip._call("hp_norm_noalloc", 6, *hip._ptrs(x, out), 3, 2048 << 19, 1)
         assert _pool(hip) == before
-    assert 3 * (1 << 19) * 16 > SCRATCH_BYTES
