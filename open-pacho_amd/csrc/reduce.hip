@@ -168,11 +168,11 @@ template <typename T, int OP>
 void run_cols(hp_ctx* ctx, const T* x, T* out, int64_t outer, int64_t reduced, int64_t inner) {
   const int v_in = hps::vector_width(x, inner, sizeof(T));
   const int v_acc = hps::vector_width(reinterpret_cast<const void*>(256), inner, sizeof(T));
-  // Sums fold with one add per element and stream best from 2 workgroups per
-  // compute unit; the NaN- and signed-zero-aware extrema fold with several
-  // instructions per element and need 4 to hide them (1 GiB float32 axis 0,
-  // one MI355X: sum 72% of HBM at 2 vs 70% at 4; max 53% at 2 vs 62% at 4).
-  const int64_t groups_per_cu = OP == HP_SUM ? 2 : 4;
+  // 2 workgroups per compute unit for every operation: with 16 loads in
+  // flight per lane the extrema's folds (two elements per v_maximum3_f32)
+  // hide behind them too (1 GiB float32 axis 0, one MI355X: max 84.3% of HBM
+  // at 2 against 81.3% at 4; sum 84.2%).
+  const int64_t groups_per_cu = 2;
   const hps::Plan plan = hps::plan(outer, reduced, inner, v_in, v_acc, sizeof(T), ctx->compute_units, groups_per_cu);
   void* buffers[2] = {nullptr, nullptr};
   for (int i = 0; i < 2; ++i)

@@ -36,23 +36,30 @@ constexpr int kThreads = 256;
 //   Out finish(Acc)                final value of a column
 // with types In, Acc, Out and the batch size kBatch.
 
-template <typename In, int V>
-__device__ __forceinline__ void load_row(const In* p, In (&v)[V], bool stream) {
+// STREAM: nontemporal loads (a first pass over HBM data read once). A
+// compile-time choice: a runtime select between the two load forms compiled
+// to plain loads.
+template <typename In, int V, bool STREAM>
+__device__ __forceinline__ void load_row(const In* p, In (&v)[V]) {
   if constexpr (V > 1) {
     static_assert(sizeof(In) * V == 16, "vector loads are 16 bytes");
     typedef unsigned int U4 __attribute__((ext_vector_type(4)));
-    const U4 bits = stream ? __builtin_nontemporal_load(reinterpret_cast<const U4*>(p)) : *reinterpret_cast<const U4*>(p);
+    U4 bits;
+    if constexpr (STREAM) bits = __builtin_nontemporal_load(reinterpret_cast<const U4*>(p));
+    else bits = *reinterpret_cast<const U4*>(p);
     __builtin_memcpy(&v[0], &bits, 16);
+  } else if constexpr (STREAM) {
+    v[0] = __builtin_nontemporal_load(p);
   } else {
     v[0] = *p;
   }
 }
 
-template <class Op, int V>
+template <class Op, int V, bool STREAM>
 __global__ __launch_bounds__(kThreads) void strided_kernel(const typename Op::In* __restrict__ x, void* __restrict__ out,
                                                            int64_t reduced, int64_t inner, int64_t col_blocks,
                                                            int64_t chunks, int64_t rows_per_chunk, int cw,
-                                                           int final_pass, int stream) {
+                                                           int final_pass) {
   using In = typename Op::In;
   using Acc = typename Op::Acc;
   constexpr int B = Op::kBatch;
@@ -74,13 +81,19 @@ __global__ __launch_bounds__(kThreads) void strided_kernel(const typename Op::In
     const int64_t end = begin + rows_per_chunk < reduced ? begin + rows_per_chunk : reduced;
     const In* base = x + o * reduced * inner + col;
     int64_t r = begin + ro;
-    // Full batches: every row of the batch is inside the chunk. The next
-    // batch's loads are issued before this one is folded (two register sets
-    // that swap roles), so each wave keeps loads in flight while it folds.
-    auto full = [&](int64_t row) { return row + int64_t(B - 1) * step < end; };
+    // Full batches, in ascending order, two register sets that swap roles:
+    // the next batch's loads are issued before this one is folded. No exit
+    // branch sits between a load and its fold: the loop takes batches in
+    // pairs with its test at the bottom, and an odd last batch is folded
+    // after it. (With an exit between them the compiler sank the lookahead
+    // loads below the fold, or waited for every load before each fold.)
+    // The lookahead of the last pair reloads the last batch, unused.
+    // The fence keeps the scheduler from spreading a batch's loads among
+    // the fold's instructions, which left half as many loads in flight.
     auto load = [&](int64_t row, In (&vals)[B][V]) {
 #pragma unroll
-      for (int j = 0; j < B; ++j) load_row<In, V>(base + (row + int64_t(j) * step) * inner, vals[j], stream != 0);
+      for (int j = 0; j < B; ++j) load_row<In, V, STREAM>(base + (row + int64_t(j) * step) * inner, vals[j]);
+      __builtin_amdgcn_sched_barrier(0);
     };
     auto fold = [&](const In (&vals)[B][V]) {
 #pragma unroll
@@ -91,20 +104,22 @@ __global__ __launch_bounds__(kThreads) void strided_kernel(const typename Op::In
         acc[v] = Op::fold(acc[v], column);
       }
     };
-    if (full(r)) {
+    const int64_t rows = r < end ? (end - r + step - 1) / step : 0;
+    const int64_t batches = rows / B, stride = int64_t(B) * step;
+    if (batches > 0) {
+      const int64_t last = r + (batches - 1) * stride;
       In set0[B][V], set1[B][V];
       load(r, set0);
-      for (;;) {
-        int64_t next = r + int64_t(B) * step;
-        if (full(next)) load(next, set1);
+      for (int64_t i = 0; i + 1 < batches; i += 2) {
+        load(r + stride, set1);
         fold(set0);
-        r = next;
-        if (!full(r)) break;
-        next = r + int64_t(B) * step;
-        if (full(next)) load(next, set0);
+        load(r + 2 * stride < last ? r + 2 * stride : last, set0);
         fold(set1);
-        r = next;
-        if (!full(r)) break;
+        r += 2 * stride;
+      }
+      if (batches & 1) {
+        fold(set0);
+        r += stride;
       }
     }
     if (r < end) {  // last partial batch: rows past the end read as identity
@@ -113,7 +128,7 @@ __global__ __launch_bounds__(kThreads) void strided_kernel(const typename Op::In
       for (int j = 0; j < B; ++j) {
         const int64_t row = r + int64_t(j) * step;
         if (row < end) {
-          load_row<In, V>(base + row * inner, vals[j], stream != 0);
+          load_row<In, V, STREAM>(base + row * inner, vals[j]);
         } else {
 #pragma unroll
           for (int v = 0; v < V; ++v) vals[j][v] = Op::identity_in();
@@ -206,15 +221,32 @@ constexpr int64_t kGroupsPerCU = 4;
 // callers.
 constexpr int64_t kMaxPartialBytes = int64_t(8) << 20;
 
+// A merge pass over at most kThreads * kOnePassRows rows finishes in one
+// launch: its column blocks narrow (cw threads across, kThreads / cw rows per
+// step) until each thread folds at most kOnePassRows rows, and the rows of
+// one step meet in the LDS tree. Two launches of full-width blocks took 9-11
+// us after a 1 GiB axis-0 pass, one narrow launch about half of that.
+constexpr int64_t kOnePassRows = 32;
+
 inline Pass plan_pass(int64_t outer, int64_t reduced, int64_t inner, int V, int64_t groups_wanted,
-                      int64_t min_rows, int64_t acc_bytes, bool cap_partials) {
+                      int64_t min_rows, int64_t acc_bytes, bool cap_partials, bool one_pass = false) {
   Pass p;
   p.V = V;
   p.reduced = reduced;
   const int64_t groups = hp::ceil_div(inner, V);
-  p.cw = int(groups < kThreads ? groups : kThreads);
+  int64_t cw = groups < kThreads ? groups : kThreads;
+  if (one_pass) {
+    const int64_t cap = kThreads / hp::ceil_div(reduced, kOnePassRows);  // >= 1 by the caller's bound
+    while (cw > cap) cw = (cw + 1) / 2;
+  }
+  p.cw = int(cw);
   p.col_blocks = hp::ceil_div(groups, p.cw);
   const int64_t step = kThreads / p.cw;
+  if (one_pass) {
+    p.rows_per_chunk = hp::ceil_div(reduced, step) * step;
+    p.chunks = 1;
+    return p;
+  }
   const int64_t blocks = outer * p.col_blocks;
   int64_t chunks = groups_wanted / blocks;
   if (chunks < 1) chunks = 1;
@@ -246,9 +278,10 @@ inline Plan plan(int64_t outer, int64_t reduced, int64_t inner, int V_in, int V_
   int64_t rows = reduced;
   for (;;) {
     const bool first = plan.count == 0;
+    const bool one_pass = !first && rows <= kThreads * kOnePassRows;
     Pass p = plan_pass(outer, rows, inner, first ? V_in : V_acc,
                        compute_units * (first ? first_groups_per_cu : kGroupsPerCU), first ? kFirstRows : kMergeRows,
-                       acc_bytes, first);
+                       acc_bytes, first, one_pass);
     hp::require(plan.count < 12, "strided reduction needs too many passes");
     hp::require(outer * p.col_blocks * p.chunks <= hp::kMaxGrid, "strided reduction too large for one launch");
     plan.passes[plan.count] = p;
@@ -273,13 +306,13 @@ inline int vector_width(const void* base, int64_t inner, int64_t elem) {
   return V;
 }
 
-template <class Op, int V>
+template <class Op, int V, bool STREAM>
 void launch_pass(hipStream_t stream, const Pass& p, const void* in, void* out, int64_t outer, int64_t inner,
-                 bool final_pass, bool streaming) {
+                 bool final_pass) {
   const int64_t grid = outer * p.col_blocks * p.chunks;
-  strided_kernel<Op, V><<<grid, kThreads, 0, stream>>>(static_cast<const typename Op::In*>(in), out, p.reduced, inner,
-                                                      p.col_blocks, p.chunks, p.rows_per_chunk, p.cw,
-                                                      final_pass ? 1 : 0, streaming ? 1 : 0);
+  strided_kernel<Op, V, STREAM><<<grid, kThreads, 0, stream>>>(static_cast<const typename Op::In*>(in), out,
+                                                               p.reduced, inner, p.col_blocks, p.chunks,
+                                                               p.rows_per_chunk, p.cw, final_pass ? 1 : 0);
   hp::check_launch("strided_reduce");
 }
 
@@ -303,11 +336,11 @@ void execute(hipStream_t stream, const Plan& plan, const typename FirstOp::In* x
     const bool final_pass = i == plan.count - 1;
     void* target = final_pass ? static_cast<void*>(out) : buffers[i % 2];
     if (i == 0) {
-      if (p.V == V_first && V_first > 1) launch_pass<FirstOp, V_first>(stream, p, source, target, outer, inner, final_pass, true);
-      else launch_pass<FirstOp, 1>(stream, p, source, target, outer, inner, final_pass, true);
+      if (p.V == V_first && V_first > 1) launch_pass<FirstOp, V_first, true>(stream, p, source, target, outer, inner, final_pass);
+      else launch_pass<FirstOp, 1, true>(stream, p, source, target, outer, inner, final_pass);
     } else {
-      if (p.V == V_merge && V_merge > 1) launch_pass<MergeOp, V_merge>(stream, p, source, target, outer, inner, final_pass, false);
-      else launch_pass<MergeOp, 1>(stream, p, source, target, outer, inner, final_pass, false);
+      if (p.V == V_merge && V_merge > 1) launch_pass<MergeOp, V_merge, false>(stream, p, source, target, outer, inner, final_pass);
+      else launch_pass<MergeOp, 1, false>(stream, p, source, target, outer, inner, final_pass);
     }
     source = target;
   }

@@ -36,8 +36,8 @@ CASES = [
     # one chunk per row (no workspace), strided axis, empty reduced axis
     (np.float32, [(4096, 4096, 1), (17, 100, 1)]),
     (np.float32, [(64, 300, 129), (3, 7, 5)]),
-    # strided axis over three passes: the first pass's pairs in the first
-    # half of the workspace, the second pass's in the half after it
+    # strided axis, long: 512 chunks of pairs from the first pass, merged by
+    # one narrow-block pass; the second call's plan differs in every extent
     (np.float32, [(1, 32768, 1024), (2, 20000, 640)]),
     (np.float64, [(5, 0, 3), (2, 0, 1)]),
 ]
