@@ -189,6 +189,13 @@ int hp_gemv_residual(hp_ctx* ctx, int dtype, const void* a, const void* x, const
  * _cuda.py:449-491 reduce). */
 int hp_dot(hp_ctx* ctx, int dtype, const void* x, const void* y, void* out, int64_t n);
 
+/* hp_dot into a new pool block: *out = a fresh allocation of one element
+ * (release it with hp_free) holding sum_i x[i] * y[i]. One call instead of
+ * hp_alloc + hp_dot, for a host path whose cost is the calls themselves.
+ * Replaces: _cuda.py:241-256 (empty of the 0-d result) with
+ * _cuda_gemv.py:47-95 (the dot into it). */
+int hp_dot_new(hp_ctx* ctx, int dtype, const void* x, const void* y, int64_t n, void** out);
+
 /* ---- reductions ---------------------------------------------------------- */
 
 /* Euclidean norm over the middle axis of x viewed as (outer, reduced, inner):

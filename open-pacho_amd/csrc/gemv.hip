@@ -265,22 +265,43 @@ int hp_gemv_residual(hp_ctx* ctx, int dtype, const void* a, const void* x, const
   });
 }
 
+static void dot_entry(hp_ctx* ctx, int dtype, const void* x, const void* y, void* out, int64_t n) {
+  require(out != nullptr, "null output");
+  if (n == 0) {
+    HP_CHECK(hipMemsetAsync(out, 0, hp::dtype_size(dtype), ctx->stream));
+    return;
+  }
+  require(x != nullptr && y != nullptr, "null input");
+  if (dtype == HP_F32) {
+    run_dot<float>(ctx, (const float*)x, (const float*)y, (float*)out, n);
+  } else {
+    run_dot<double>(ctx, (const double*)x, (const double*)y, (double*)out, n);
+  }
+}
+
 int hp_dot(hp_ctx* ctx, int dtype, const void* x, const void* y, void* out, int64_t n) {
   return guarded([&] {
     hp::enter(ctx);
     require(dtype == HP_F32 || dtype == HP_F64, "dot supports float32 and float64");
     require(n >= 0, "negative length");
+    dot_entry(ctx, dtype, x, y, out, n);
+  });
+}
+
+int hp_dot_new(hp_ctx* ctx, int dtype, const void* x, const void* y, int64_t n, void** out) {
+  return guarded([&] {
+    hp::enter(ctx);
     require(out != nullptr, "null output");
-    if (n == 0) {
-      HP_CHECK(hipMemsetAsync(out, 0, hp::dtype_size(dtype), ctx->stream));
-      return;
+    require(dtype == HP_F32 || dtype == HP_F64, "dot supports float32 and float64");
+    require(n >= 0, "negative length");
+    void* block = hp::scratch_alloc(ctx, hp::dtype_size(dtype));
+    try {
+      dot_entry(ctx, dtype, x, y, block, n);
+    } catch (...) {
+      hp::scratch_free(ctx, block);
+      throw;
     }
-    require(x != nullptr && y != nullptr, "null input");
-    if (dtype == HP_F32) {
-      run_dot<float>(ctx, (const float*)x, (const float*)y, (float*)out, n);
-    } else {
-      run_dot<double>(ctx, (const double*)x, (const double*)y, (double*)out, n);
-    }
+    *out = block;
   });
 }
 

@@ -604,6 +604,16 @@ def matmul(a, b, *, padding=False):
 
 @_implements(np.dot)
 def dot(a, b):
+    if type(a) is ndarray and type(b) is ndarray and len(a._shape) == 1 == len(b._shape):
+        # Two vectors of one backend, dtype and length: a backend that offers
+        # a one-call vector dot skips the product dispatch (the same 0-d
+        # result as the matmul below).
+        fast = getattr(a._backend, "vector_dot", None)
+        if fast is not None and a._backend is b._backend and a._dtype == b._dtype and a._dtype.kind == "f":
+            if a._shape == b._shape and a._shape[0]:
+                result = object.__new__(ndarray)
+                result._data, result._shape, result._dtype, result._backend = fast(a, b), (), a._dtype, a._backend
+                return result
     ranks = [v.ndim if isinstance(v, ndarray) else np.ndim(v) for v in (a, b)]
     if 0 in ranks:
         return _elementwise(np.multiply, a, b)

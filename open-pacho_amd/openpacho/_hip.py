@@ -20,7 +20,7 @@ import ctypes
 from collections import OrderedDict
 from math import prod
 from threading import RLock
-from weakref import WeakSet
+import weakref
 
 import numpy as np
 
@@ -81,7 +81,7 @@ class _Allocation:
         self.backend = backend
         self.ptr = int(ptr)
         self.capacity = capacity
-        backend._leases.add(self)
+        backend._lease(self)
 
     def __del__(self):
         try:
@@ -135,6 +135,7 @@ class HIPBackend:
     name = "hip"
     blas = "custom"
     fp64 = True
+    _is_tracing = False  # a class attribute: the facade probes it on every result
     # One fused step cannot amortise entering a scope; plans of >= 2 launches do.
     execution_scope_min_steps = 2
 
@@ -142,7 +143,11 @@ class HIPBackend:
         self._lib = lib_.load()
         self._lock = RLock()
         self._guard = _Active(self)
-        self._leases = WeakSet()
+        # Weak references to the live allocations, zeroed by close(): plain
+        # references in a list (a WeakSet entry costs a callback per
+        # allocation), dead ones dropped whenever the list doubles.
+        self._leases = []
+        self._lease_prune_at = 1024
         self._kernels = OrderedDict()
         self._ctx = None
         self._closed = False
@@ -160,6 +165,9 @@ class HIPBackend:
             raise BackendUnavailableError(f"HIP initialization failed: {lib_.last_error(self._lib)}")
         self._ctx = ctx
         self._pool_limit = self.device_info.memory_bytes // 4  # hp_init's default
+        # Bound once: the calls of the shortest operations are their cost.
+        self._free = self._lib.hp_free
+        self._dot_new = self._lib.hp_dot_new
 
     # ---- plumbing ---------------------------------------------------------------
 
@@ -176,10 +184,18 @@ class HIPBackend:
         """Hold the backend lock for one plan execution."""
         return self._active()
 
+    def _lease(self, allocation):
+        """Record a new allocation (called with the backend lock held)."""
+        leases = self._leases
+        leases.append(weakref.ref(allocation))
+        if len(leases) >= self._lease_prune_at:
+            self._leases = [ref for ref in leases if ref() is not None]
+            self._lease_prune_at = max(1024, 2 * len(self._leases))
+
     def _release(self, ptr):
         with self._lock:
             if not self._closed:
-                self._lib.hp_free(self._ctx, ctypes.c_void_p(ptr))
+                self._free(self._ctx, ptr)
 
     def _launch(self, source, name, grid, operands, out):
         """Compile (cached) and launch an RTC kernel over operands + out."""
@@ -400,6 +416,20 @@ class HIPBackend:
         self._gemm(code, a, b, out, m, n, k, batch, a_batch, b.shape[:-2])
         return out
 
+    def vector_dot(self, a, b):
+        """Storage of the 0-d a . b of two non-empty 1-D float vectors of one
+        dtype and length: the result's allocation and the launch are one
+        library call. A short dot costs its host calls, not its kernel."""
+        dtype = a._dtype
+        ptr = ctypes.c_void_p()
+        with self._lock:
+            if self._closed:
+                raise RuntimeError("hip backend is closed")
+            status = self._dot_new(self._ctx, lib_.DTYPE_CODES[dtype], a._data.ptr, b._data.ptr, a._shape[0], ptr)
+            if status:
+                lib_.check(self._lib, status, "hp_dot_new")
+            return _Allocation(self, ptr.value, dtype.itemsize)
+
     def _gemm(self, code, a, b, out, m, n, k, batch, a_batch, b_batch):
         dims, a_strides, b_strides = self._batch_strides(batch, a_batch, m * k, b_batch, k * n)
         with self._active():
@@ -549,8 +579,11 @@ class HIPBackend:
         with self._lock:
             if self._closed:
                 return
-            for lease in list(self._leases):
-                lease.ptr = 0
+            for ref in self._leases:
+                lease = ref()
+                if lease is not None:
+                    lease.ptr = 0
+            self._leases = []
             for kernel in self._kernels.values():
                 self._lib.hp_rtc_release(self._ctx, kernel)
             self._kernels.clear()

@@ -58,6 +58,7 @@ PROTOTYPES = {
     "hp_gemv": [_ptr, _i32, _ptr, _ptr, _ptr, _i64, _i64],
     "hp_gemv_residual": [_ptr, _i32, _ptr, _ptr, _ptr, _ptr, _i64, _i64],
     "hp_dot": [_ptr, _i32, _ptr, _ptr, _ptr, _i64],
+    "hp_dot_new": [_ptr, _i32, _ptr, _ptr, _i64, _pptr],
     "hp_norm": [_ptr, _i32, _ptr, _ptr, _i64, _i64, _i64],
     "hp_norm_noalloc": [_ptr, _i32, _ptr, _ptr, _i64, _i64, _i64],
     "hp_reduce": [_ptr, _i32, _i32, _ptr, _ptr, _i64, _i64, _i64],

@@ -69,6 +69,8 @@ class NumpyBackend:
     Storage is a flat C-order NumPy array; the array facade keeps the shape.
     """
 
+    _is_tracing = False
+
     name = "numpy"
     device = "CPU (NumPy)"
     fp64 = True

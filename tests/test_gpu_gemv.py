@@ -69,6 +69,27 @@ def test_gemv_cancellation_large_finite_signed_and_nonfinite(hip, dtype):
     assert np.isnan(values[3]) and np.isneginf(values[4])
 
 
+@pytest.mark.parametrize("dtype", [np.float32, np.float64])
+@pytest.mark.parametrize("poison", [np.nan, np.inf])
+def test_dot_result_block_is_written_not_read(hip, dtype, poison):
+    """p.dot's 0-d result is a new pool block that the kernel only writes
+    (reference tests/test_cuda.py:345-391 for products): the block it reuses
+    is poisoned first, and every call gets a fresh one."""
+    x = p.asarray(np.arange(1, 4097, dtype=dtype) / 4096, backend=hip)
+    want = float(exact.exact_dot(p.asnumpy(x), p.asnumpy(x)))
+    hip.release_cached_memory()  # the poisoned block is then the only cached one of its size
+    block = p.full((), poison, dtype=dtype, backend=hip)
+    address = block._data.ptr
+    del block
+    first = p.dot(x, x)
+    assert first._data.ptr == address
+    assert first.shape == () and first.dtype == dtype
+    assert float(p.asnumpy(first)) == pytest.approx(want, rel=1e-6)
+    second = p.dot(x, x)
+    assert second._data is not first._data and second._data.ptr != first._data.ptr
+    assert p.asnumpy(second).tobytes() == p.asnumpy(first).tobytes()
+
+
 def test_empty_and_zero_inner(hip):
     for dtype in (np.float32, np.float64):
         empty = p.asarray(np.zeros((0, 64), dtype), backend=hip) @ p.asarray(np.zeros(64, dtype), backend=hip)
