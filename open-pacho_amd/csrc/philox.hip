@@ -51,6 +51,63 @@ __device__ __forceinline__ Words philox10(uint32_t c0, uint32_t c1, uint32_t c2,
   return {c0, c1, c2, c3};
 }
 
+// The same ten rounds for a counter block (lo + J, hi, 0, 0) whose high word
+// hi is wave-uniform and lo + J does not carry (the kernel's common path),
+// arranged so that the wave-uniform values stay on the scalar unit:
+// round 1's c2 product is zero and its new c0 = hi ^ k0 is uniform, so round
+// 2's c0 product is a scalar multiply whose low word, c3 of round 3, is
+// uniform too. Uniform XORs are written with ^ (a scalar instruction; the
+// three-input builtin would force them onto the vector unit, and gfx9 vector
+// instructions read one scalar register at most). J rides in round 1's
+// multiply-add: (lo + J) M0 = lo M0 + J M0 with no carry out of 64 bits.
+// m0 is M0 held in a vector register, so that the multiply-add's one scalar
+// operand is the 64-bit addend J M0 (with M0 in a scalar register the
+// compiler moved the addend into two vector registers per sample).
+template <int J>
+__device__ __forceinline__ Words philox10_uniform_hi(uint32_t lo, uint32_t m0, uint32_t hi, uint32_t k0,
+                                                     uint32_t k1) {
+  // Round 1.
+  const uint64_t a0 = uint64_t(lo) * m0 + uint64_t(J) * kM0;
+  uint32_t c0 = hi ^ k0;
+  uint32_t c2 = uint32_t(a0 >> 32) ^ k1;
+  uint32_t c3 = uint32_t(a0);
+  k0 += kW0;
+  k1 += kW1;
+  // Round 2 (c1 = 0).
+  const uint64_t p0 = uint64_t(c0) * kM0;
+  const uint64_t p1 = uint64_t(c2) * kM1;
+  c0 = uint32_t(p1 >> 32) ^ k0;
+  c2 = (uint32_t(p0 >> 32) ^ k1) ^ c3;
+  c3 = uint32_t(p0);
+  uint32_t c1 = uint32_t(p1);
+  k0 += kW0;
+  k1 += kW1;
+  // Round 3 (c3 uniform).
+  const uint64_t q0 = uint64_t(c0) * kM0;
+  const uint64_t q1 = uint64_t(c2) * kM1;
+  c0 = xor3(uint32_t(q1 >> 32), c1, k0);
+  c2 = uint32_t(q0 >> 32) ^ (c3 ^ k1);
+  c1 = uint32_t(q1);
+  c3 = uint32_t(q0);
+  k0 += kW0;
+  k1 += kW1;
+  // Rounds 4-10.
+#pragma unroll
+  for (int round = 3; round < 10; ++round) {
+    const uint64_t r0 = uint64_t(c0) * kM0;
+    const uint64_t r1 = uint64_t(c2) * kM1;
+    const uint32_t n0 = xor3(uint32_t(r1 >> 32), c1, k0);
+    const uint32_t n2 = xor3(uint32_t(r0 >> 32), c3, k1);
+    c0 = n0;
+    c1 = uint32_t(r1);
+    c2 = n2;
+    c3 = uint32_t(r0);
+    k0 += kW0;
+    k1 += kW1;
+  }
+  return {c0, c1, c2, c3};
+}
+
 template <typename T>
 __device__ __forceinline__ T unit(uint32_t a, uint32_t b);
 
@@ -119,6 +176,13 @@ __device__ __forceinline__ float transform<float, HP_EXPONENTIAL>(const Words& w
   return second * nl;
 }
 
+// 1 - u on the float32 unit grid as one fused multiply-add: u = k 2^-24 and
+// 1 - u are exact, so fma(k, -2^-24, 1) is the same value as 1 - (k 2^-24)
+// in one instruction instead of two.
+__device__ __forceinline__ float one_minus_unit(uint32_t a) {
+  return __builtin_fmaf(float(a >> 8), -5.9604644775390625e-8f, 1.0f);
+}
+
 // float32 exponential and normal with their constant factors folded on the
 // host into one normal-range float (one multiply per sample fewer; the
 // result moves by at most ~2 ulp, inside the 3e-6 stream tolerance):
@@ -129,16 +193,17 @@ constexpr int kExponentialFolded = 6, kNormalFolded = 7;
 
 template <>
 __device__ __forceinline__ float transform<float, kExponentialFolded>(const Words& w, float, float folded, float) {
-  const float u = unit<float>(w.x0, w.x1);
-  return __builtin_fabsf(__builtin_amdgcn_logf(1.0f - u)) * folded;
+  return __builtin_fabsf(__builtin_amdgcn_logf(one_minus_unit(w.x0))) * folded;
 }
 
+// loc + radius * cos as one fused multiply-add: one rounding instead of two
+// (within the stream tolerance; for loc = 0 the same value, and +0 where the
+// radius is +0, as before).
 template <>
 __device__ __forceinline__ float transform<float, kNormalFolded>(const Words& w, float first, float folded, float) {
-  const float u = unit<float>(w.x0, w.x1);
-  const float radius2 = __builtin_fabsf(__builtin_amdgcn_logf(1.0f - u)) * folded;
+  const float radius2 = __builtin_fabsf(__builtin_amdgcn_logf(one_minus_unit(w.x0))) * folded;
   const float v = unit<float>(w.x2, w.x3);
-  return first + __builtin_amdgcn_sqrtf(radius2) * __builtin_amdgcn_cosf(v);
+  return __builtin_fmaf(__builtin_amdgcn_sqrtf(radius2), __builtin_amdgcn_cosf(v), first);
 }
 
 // Uniform with the width pre-scaled by the unit's power of two, selected by
@@ -184,34 +249,40 @@ __device__ __forceinline__ double transform<double, kUniformScaledZero>(const Wo
   return (double(w.x0 >> 5) * 67108864.0 + double(w.x1 >> 6)) * scaled;
 }
 
-template <typename T>
-__device__ __forceinline__ void store4(T* out, int64_t e0, int64_t count, const T (&v)[4]);
-
-template <>
-__device__ __forceinline__ void store4<float>(float* out, int64_t e0, int64_t count, const float (&v)[4]) {
-  if (e0 + 3 < count) {
-    hpd::f32x4 q = {v[0], v[1], v[2], v[3]};
-    *reinterpret_cast<hpd::f32x4*>(out + e0) = q;
-  } else {
-    for (int j = 0; j < 4; ++j)
-      if (e0 + j < count) out[e0 + j] = v[j];
-  }
-}
-
-template <>
-__device__ __forceinline__ void store4<double>(double* out, int64_t e0, int64_t count, const double (&v)[4]) {
-  if (e0 + 3 < count) {
-    hpd::f64x2 a = {v[0], v[1]}, b = {v[2], v[3]};
-    reinterpret_cast<hpd::f64x2*>(out + e0)[0] = a;
-    reinterpret_cast<hpd::f64x2*>(out + e0)[1] = b;
-  } else {
-    for (int j = 0; j < 4; ++j)
-      if (e0 + j < count) out[e0 + j] = v[j];
-  }
-}
-
 constexpr int kBlock = 256;
-constexpr int kPerThread = 4;
+// Samples per thread: eight consecutive counters, stored as 16-byte vectors;
+// the per-thread work around the blocks (counter base, tail test, address)
+// is then shared by eight samples (with four it added ~1.5 instructions per
+// sample).
+constexpr int kPerThread = 8;
+
+// values[0 .. kPerThread) to out[e0 ..), vector stores when all are inside.
+template <typename T>
+__device__ __forceinline__ void store_run(T* out, int64_t e0, int64_t count, const T (&v)[kPerThread]) {
+  if (e0 + kPerThread <= count) {
+    if constexpr (sizeof(T) == 4) {
+#pragma unroll
+      for (int q = 0; q < kPerThread / 4; ++q)
+        reinterpret_cast<hpd::f32x4*>(out + e0)[q] = hpd::f32x4{v[4 * q], v[4 * q + 1], v[4 * q + 2], v[4 * q + 3]};
+    } else {
+#pragma unroll
+      for (int q = 0; q < kPerThread / 2; ++q) reinterpret_cast<hpd::f64x2*>(out + e0)[q] = hpd::f64x2{v[2 * q], v[2 * q + 1]};
+    }
+  } else {
+    for (int j = 0; j < kPerThread; ++j)
+      if (e0 + j < count) out[e0 + j] = v[j];
+  }
+}
+
+// values[J ..) of a run whose counters (lo0 + j, hi) share the wave-uniform hi.
+template <typename T, int DIST, int J = 0>
+__device__ __forceinline__ void run_uniform_hi(T (&values)[kPerThread], uint32_t lo0, uint32_t m0, uint32_t hi,
+                                               uint32_t k0, uint32_t k1, T first, T second, T upper) {
+  if constexpr (J < kPerThread) {
+    values[J] = transform<T, DIST>(philox10_uniform_hi<J>(lo0, m0, hi, k0, k1), first, second, upper);
+    run_uniform_hi<T, DIST, J + 1>(values, lo0, m0, hi, k0, k1, first, second, upper);
+  }
+}
 
 template <typename T, int DIST>
 __global__ __launch_bounds__(kBlock) void philox_kernel(T* __restrict__ out, int64_t count, uint32_t k0,
@@ -223,16 +294,13 @@ __global__ __launch_bounds__(kBlock) void philox_kernel(T* __restrict__ out, int
   const uint64_t wave_last = wave_first + (64 * kPerThread - 1);
   const int64_t e0 = block_first + int64_t(threadIdx.x) * kPerThread;
   if (e0 >= count) return;
-  T values[4];
+  T values[kPerThread];
   if (uint32_t(wave_first >> 32) == uint32_t(wave_last >> 32)) {
     // Wave-uniform high word: no carry inside this wave's counters.
-    const uint32_t hi = uint32_t(wave_first >> 32);
-    const uint32_t lo0 = uint32_t(start) + uint32_t(e0);
-#pragma unroll
-    for (int j = 0; j < kPerThread; ++j) {
-      const Words w = philox10(lo0 + uint32_t(j), hi, 0u, 0u, k0, k1);
-      values[j] = transform<T, DIST>(w, first, second, upper);
-    }
+    uint32_t m0;
+    asm("v_mov_b32 %0, 0xd2511f53" : "=v"(m0));  // kM0, in a vector register
+    run_uniform_hi<T, DIST>(values, uint32_t(start) + uint32_t(e0), m0, uint32_t(wave_first >> 32), k0, k1, first,
+                            second, upper);
   } else {
 #pragma unroll
     for (int j = 0; j < kPerThread; ++j) {
@@ -241,7 +309,7 @@ __global__ __launch_bounds__(kBlock) void philox_kernel(T* __restrict__ out, int
       values[j] = transform<T, DIST>(w, first, second, upper);
     }
   }
-  store4<T>(out, e0, count, values);
+  store_run<T>(out, e0, count, values);
 }
 
 __global__ __launch_bounds__(kBlock) void philox_words_kernel(uint32_t* __restrict__ out, int64_t count,
