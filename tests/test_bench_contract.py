@@ -55,17 +55,27 @@ def test_profile_tables_name_built_kernels():
 
 
 def test_warm_up_runs_the_minimum_calls_and_the_minimum_time(monkeypatch):
+    """At least `calls` calls and WARM_MS of time; after the first call the
+    calls are queued in batches of about 5 ms of work, synchronized between
+    batches only (a sync after every call left the device idle)."""
     monkeypatch.setattr(bench, "WARM_MS", 30.0)
-    calls, syncs = [], []
+    events = []
+
+    def call():
+        events.append("c")
+        bench.time.sleep(0.001)  # ~1 ms of "device work": batches of ~5
+
     start = bench.time.perf_counter()
-    bench.warm(lambda: calls.append(1), lambda: syncs.append(1), 3)
+    bench.warm(call, lambda: events.append("s"), 3)
     elapsed_ms = (bench.time.perf_counter() - start) * 1e3
-    assert len(calls) >= 3 and len(syncs) == len(calls)
-    assert elapsed_ms >= 30.0
+    assert elapsed_ms >= 30.0 and events[:2] == ["c", "s"] and events[-1] == "s"
+    batches = "".join(events[2:]).split("s")[:-1]
+    assert batches and all(b == batches[0] for b in batches) and 2 <= len(batches[0]) <= 5
+    assert events.count("c") >= 3 and events.count("s") < events.count("c")
     monkeypatch.setattr(bench, "WARM_MS", 0.0)
-    calls.clear()
-    bench.warm(lambda: calls.append(1), lambda: None, 5)
-    assert len(calls) == 5
+    events.clear()
+    bench.warm(call, lambda: events.append("s"), 5)
+    assert events.count("c") >= 5
 
 
 def test_cpu_baseline_protocol_warms_then_takes_the_median_of_seven():
