@@ -225,8 +225,9 @@ constexpr int64_t kMaxPartialBytes = int64_t(8) << 20;
 // launch: its column blocks narrow (cw threads across, kThreads / cw rows per
 // step) until each thread folds at most kOnePassRows rows, and the rows of
 // one step meet in the LDS tree. Two launches of full-width blocks took 9-11
-// us after a 1 GiB axis-0 pass, one narrow launch about half of that.
-constexpr int64_t kOnePassRows = 32;
+// us after a 1 GiB axis-0 pass, one narrow launch about half of that (16
+// rows per thread against 32: the norm's pair merges +0.5% of HBM).
+constexpr int64_t kOnePassRows = 16;
 
 inline Pass plan_pass(int64_t outer, int64_t reduced, int64_t inner, int V, int64_t groups_wanted,
                       int64_t min_rows, int64_t acc_bytes, bool cap_partials, bool one_pass = false) {
