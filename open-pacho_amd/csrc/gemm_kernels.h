@@ -1643,38 +1643,59 @@ __global__ __launch_bounds__(kThreads, 1) void kernel(const double* __restrict__
 
 // Adds the cut pieces of each stream-K tile in K order (workers in increasing
 // order own increasing K ranges) and stores the tile. Tiles that one worker
-// covered whole were stored by it. One thread per accumulator 4-vector.
+// covered whole were stored by it. A thread handles kFixupVectors
+// accumulator 4-vectors kFixupThreads apart (loads of all its pieces issued
+// before the adds); a workgroup covers kFixupThreads * kFixupVectors vectors
+// of one tile.
+constexpr int kFixupThreads = 256;
+constexpr int kFixupVectors = 4;
+
 template <typename T, typename V, typename L>
-__global__ __launch_bounds__(256) void fixup_kernel(T* __restrict__ C, int64_t M, int64_t N, TileMap tmap,
-                                                    Split sp) {
+__global__ __launch_bounds__(kFixupThreads) void fixup_kernel(T* __restrict__ C, int64_t M, int64_t N, TileMap tmap,
+                                                              Split sp) {
   constexpr int BM = L::kBM, BN = L::kBN, FM = L::kFM, FN = L::kFN;
   constexpr int kVectors = BM * BN / 4;
-  constexpr int kBlocksPerTile = kVectors / 256;
+  constexpr int kBlocksPerTile = kVectors / (kFixupThreads * kFixupVectors);
+  static_assert(kBlocksPerTile * kFixupThreads * kFixupVectors == kVectors, "whole blocks per tile");
   const int64_t tl = blockIdx.x / kBlocksPerTile;
-  const int v = (blockIdx.x % kBlocksPerTile) * 256 + threadIdx.x;
+  const int v0 = (blockIdx.x % kBlocksPerTile) * (kFixupThreads * kFixupVectors) + threadIdx.x;
   const int64_t g0 = tl * sp.slices;
   const int64_t w0 = sk_worker(sp, g0), w1 = sk_worker(sp, g0 + sp.slices - 1);
   if (w0 == w1) return;
   const V* partial = static_cast<const V*>(sp.partial);
   // w0 holds the tile's K start: as its first piece when its run starts
   // there, else as its last. Later workers start inside the tile.
-  V sum = partial[(w0 * 2 + (sk_begin(sp, w0) == g0 ? 0 : 1)) * kVectors + v];
-  for (int64_t w = w0 + 1; w <= w1; ++w) sum = sum + partial[w * 2 * kVectors + v];
-  const int lane = v & 63;
-  const int block = v >> 6;
-  const int wave = block / (FM * FN);
-  const int i = (block / FN) % FM;
-  const int j = block % FN;
+  const int64_t first = (w0 * 2 + (sk_begin(sp, w0) == g0 ? 0 : 1)) * kVectors;
+  V sum[kFixupVectors];
+#pragma unroll
+  for (int q = 0; q < kFixupVectors; ++q) sum[q] = partial[first + v0 + q * kFixupThreads];
+  for (int64_t w = w0 + 1; w <= w1; ++w) {
+    V part[kFixupVectors];
+#pragma unroll
+    for (int q = 0; q < kFixupVectors; ++q) part[q] = partial[w * 2 * kVectors + v0 + q * kFixupThreads];
+#pragma unroll
+    for (int q = 0; q < kFixupVectors; ++q) sum[q] = sum[q] + part[q];
+  }
   int64_t batch, ti, tj;
   logical_tile(sp.dp_tiles + tl, tmap, batch, ti, tj);
   T* Cb = C + batch * M * tmap.ldc;
   // The tile was computed at its (possibly moved) origin, as in the kernels.
   const int64_t m0 = ti * BM, n0 = tj * BN;
-  const int64_t col = (sp.moved ? tile_origin(n0, N, BN) : n0) + L::col(wave, j, lane);
+  const int64_t mo = sp.moved ? tile_origin(m0, M, BM) : m0, no = sp.moved ? tile_origin(n0, N, BN) : n0;
 #pragma unroll
-  for (int r = 0; r < 4; ++r) {
-    const int64_t row = (sp.moved ? tile_origin(m0, M, BM) : m0) + L::row(wave, i, lane, r);
-    if (row >= m0 && row < M && col >= n0 && col < N) Cb[row * tmap.ldc + col] = sum[r];
+  for (int q = 0; q < kFixupVectors; ++q) {
+    const int v = v0 + q * kFixupThreads;
+    const int lane = v & 63;
+    const int block = v >> 6;
+    const int wave = block / (FM * FN);
+    const int i = (block / FN) % FM;
+    const int j = block % FN;
+    const int64_t col = no + L::col(wave, j, lane);
+#pragma unroll
+    for (int r = 0; r < 4; ++r) {
+      const int64_t row = mo + L::row(wave, i, lane, r);
+      if (row >= m0 && row < M && col >= n0 && col < N) Cb[row * tmap.ldc + col] = sum[q][r];
+    }
   }
 }
 
@@ -1792,7 +1813,8 @@ void launch_split(hp_ctx* ctx, Whole whole, Cut cut, Fix fixup, int threads, con
     sp.partial = hp::scratch_alloc(ctx, size_t(sp.workers) * 2 * BM * BN * sizeof(T));
     cut<<<sp.workers, threads, 0, ctx->stream>>>(a, b, c, m, n, k, bd, tm, sp);
     hp::check_launch(name);
-    fixup<<<(tm.total - sp.dp_tiles) * (BM * BN / 4 / 256), 256, 0, ctx->stream>>>(c, m, n, tm, sp);
+    fixup<<<(tm.total - sp.dp_tiles) * (BM * BN / 4 / (kFixupThreads * kFixupVectors)), kFixupThreads, 0, ctx->stream>>>(
+        c, m, n, tm, sp);
     hp::check_launch(name);
     hp::scratch_free(ctx, sp.partial);
   }
