@@ -10,6 +10,7 @@ at least a minimum number of untimed calls and a minimum span of untimed work.
 import json
 import subprocess
 import sys
+import types
 from pathlib import Path
 
 import pytest
@@ -59,18 +60,18 @@ def test_warm_up_runs_the_minimum_calls_and_the_minimum_time(monkeypatch):
     calls are queued in batches of about 5 ms of work, synchronized between
     batches only (a sync after every call left the device idle)."""
     monkeypatch.setattr(bench, "WARM_MS", 30.0)
+    clock = types.SimpleNamespace(now=0.0)
+    monkeypatch.setattr(bench, "time", types.SimpleNamespace(perf_counter=lambda: clock.now))
     events = []
 
     def call():
         events.append("c")
-        bench.time.sleep(0.001)  # ~1 ms of "device work": batches of ~5
+        clock.now += 0.00125  # 1.25 ms of "device work" per call: batches of 4
 
-    start = bench.time.perf_counter()
     bench.warm(call, lambda: events.append("s"), 3)
-    elapsed_ms = (bench.time.perf_counter() - start) * 1e3
-    assert elapsed_ms >= 30.0 and events[:2] == ["c", "s"] and events[-1] == "s"
+    assert clock.now * 1e3 >= 30.0 and events[:2] == ["c", "s"] and events[-1] == "s"
     batches = "".join(events[2:]).split("s")[:-1]
-    assert batches and all(b == batches[0] for b in batches) and 2 <= len(batches[0]) <= 5
+    assert batches and all(b == "cccc" for b in batches)
     assert events.count("c") >= 3 and events.count("s") < events.count("c")
     monkeypatch.setattr(bench, "WARM_MS", 0.0)
     events.clear()

@@ -669,8 +669,8 @@ def test_k_edge_of_adjacent_batch_matrices_contracts_zeros(hip, dtype, batch, m,
 # with K cut into chunks, the few-columns kernel streams A rows).
 EDGE_CASES = [
     (257, 300, 512),  # one edge row; 44 edge columns stay in tiles
-    (520, 264, 1000),  # 8 rows and 8 columns
-    (263, 1031, 77),  # 7 and 7, odd K: two K chunks of the rows strip
+    (520, 264, 1000),  # 8 rows
+    (263, 1031, 77),  # 7 rows, odd K: two K chunks of the rows strip
     (1280, 513, 3001),  # one edge column, odd K
     (4097, 4097, 16),  # one row and one column, one K slice (rows strip written directly)
     (300, 2305, 4096),  # one edge column beside 44 rows in tiles
@@ -733,6 +733,33 @@ def test_edge_strips_against_float64_and_repeatable(hip, m, k, n):
         hip_strip = np.sqrt(np.mean(((got[rr, cc] - truth) / mag) ** 2))
         ref_strip = np.sqrt(np.mean(((ref - truth) / mag) ** 2))
         assert hip_strip <= 2 * ref_strip + 2.0**-24
+
+
+# Strips in every operand layout: one code path over strides, one sum order,
+# so a product of transposed operands equals the product of the materialized
+# transposes bit for bit. (m, k, n): 7 rows and 7 columns; 8 and 8 over
+# several K chunks of the rows strip; 2 columns with a K tail of 4 and no
+# rows strip.
+STRIP_LAYOUT_CASES = [(263, 1031, 263), (520, 2600, 1032), (1290, 4100, 770)]
+
+
+@pytest.mark.parametrize("ta,tb", LAYOUTS)
+@pytest.mark.parametrize("m,k,n", STRIP_LAYOUT_CASES)
+def test_edge_strips_in_every_layout_match_materialized_transposes(hip, ta, tb, m, k, n):
+    rng = np.random.default_rng(7 * m + k + 3 * n + 2 * ta + tb)
+    left = rng.uniform(-1, 1, (k, m) if ta else (m, k)).astype(np.float32)
+    right = rng.uniform(-1, 1, (n, k) if tb else (k, n)).astype(np.float32)
+    a, b = p.asarray(left, backend=hip), p.asarray(right, backend=hip)
+    product = p.compile(lambda x, y: (x.T if ta else x) @ (y.T if tb else y))
+    got = p.asnumpy(product(a, b))
+    np.testing.assert_array_equal(got, p.asnumpy(product(a, b)))
+    op_a, op_b = (left.T if ta else left), (right.T if tb else right)
+    plain_a = p.asarray(np.ascontiguousarray(op_a), backend=hip)
+    plain = p.asnumpy(plain_a @ p.asarray(np.ascontiguousarray(op_b), backend=hip))
+    np.testing.assert_array_equal(got, plain)
+    want = op_a.astype(np.float64) @ op_b.astype(np.float64)
+    scale = np.abs(op_a).astype(np.float64) @ np.abs(op_b).astype(np.float64)
+    assert np.all(np.abs(got - want) <= 4e-7 * np.sqrt(k) * 4 * scale + 1e-30)
 
 
 def _tile_rows_ratio(A, C, b, r0, r1):
