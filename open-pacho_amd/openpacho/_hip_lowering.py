@@ -33,10 +33,23 @@ _CTYPE = {
 _UNSIGNED = {np.dtype("int32"): "unsigned int", np.dtype("int64"): "unsigned long long"}
 
 BLOCK = 256
-ELEMENTS_PER_THREAD = 4
+ELEMENTS_PER_THREAD = 4  # groups of VECTOR consecutive elements per thread
+VECTOR = 4
 REDUCE_CHUNK = 8192
 
 _PRELUDE = r"""
+// Four consecutive elements at p, aligned to four elements (one vector access).
+template <typename T> __device__ __forceinline__ void pacho_load4(const T* __restrict__ p, T (&v)[4]) {
+  typedef T V __attribute__((ext_vector_type(4)));
+  const V x = *reinterpret_cast<const V*>(p);
+  v[0] = x[0]; v[1] = x[1]; v[2] = x[2]; v[3] = x[3];
+}
+template <typename T> __device__ __forceinline__ void pacho_store4(T* __restrict__ p, const T (&v)[4]) {
+  typedef T V __attribute__((ext_vector_type(4)));
+  V x;
+  x[0] = v[0]; x[1] = v[1]; x[2] = v[2]; x[3] = v[3];
+  *reinterpret_cast<V*>(p) = x;
+}
 template <typename T> __device__ __forceinline__ T pacho_min(T a, T b) { return a < b ? a : b; }
 template <typename T> __device__ __forceinline__ T pacho_max(T a, T b) { return a > b ? a : b; }
 __device__ __forceinline__ float pacho_min(float a, float b) {
@@ -117,8 +130,10 @@ def _operation(op, resolved, out_dtype):
     return table[op]
 
 
-def _broadcast_offset(root_shape, leaf_shape, var):
-    """Element offset of ``leaf`` (right-aligned broadcast) at flat root index ``var``."""
+def _broadcast_offset(root_shape, leaf_shape, var, suffix="LL"):
+    """Element offset of ``leaf`` (right-aligned broadcast) at flat root index
+    ``var``; constants carry ``suffix`` (``LL`` for 64-bit index math, ``U``
+    for 32-bit)."""
     if tuple(leaf_shape) == tuple(root_shape):
         return var
     lead = len(root_shape) - len(leaf_shape)
@@ -128,8 +143,20 @@ def _broadcast_offset(root_shape, leaf_shape, var):
             continue
         outer = prod(root_shape[lead + axis + 1 :])
         inner = prod(leaf_shape[axis + 1 :])
-        terms.append(f"(({var} / {max(1, outer)}LL) % {extent}LL) * {inner}LL")
-    return " + ".join(terms) or "0LL"
+        terms.append(f"(({var} / {max(1, outer)}{suffix}) % {extent}{suffix}) * {inner}{suffix}")
+    return " + ".join(terms) or f"0{suffix}"
+
+
+def _rows_of_four(root_shape, leaf_shape):
+    """True when four consecutive root elements starting at a multiple of
+    four read four consecutive leaf elements: the leaf equals the root or is
+    broadcast over leading axes only, and the root's last axis holds whole
+    groups of four."""
+    if tuple(leaf_shape) == tuple(root_shape):
+        return True
+    if not leaf_shape or not root_shape or root_shape[-1] % VECTOR != 0:
+        return False
+    return leaf_shape[-1] == root_shape[-1]
 
 
 class _Leaf:
@@ -139,11 +166,13 @@ class _Leaf:
         self.scalar, self.dtype, self.shape = scalar, np.dtype(dtype), tuple(shape)
 
 
-def _body(root_shape, leaves, nodes, var="i"):
+def _body(root_shape, leaves, nodes, var="i", leaf_value=None, suffix="LL"):
     """Source lines computing each node; returns (params, lines, result symbol).
 
     ``leaves`` is a list of _Leaf; ``nodes`` a list of (op, input refs,
     resolved dtypes, out dtype) where refs index leaves (0..L-1) then nodes.
+    ``leaf_value(k)``, when given, is the expression of array leaf k's value
+    (else its load at flat index ``var``).
     """
     params, lines, names = [], [], []
     for k, leaf in enumerate(leaves):
@@ -153,7 +182,8 @@ def _body(root_shape, leaves, nodes, var="i"):
             lines.append(f"const {t} v{k} = x{k};")
         else:
             params.append(f"const {t}* __restrict__ x{k}")
-            lines.append(f"const {t} v{k} = x{k}[{_broadcast_offset(root_shape, leaf.shape, var)}];")
+            value = leaf_value(k) if leaf_value else f"x{k}[{_broadcast_offset(root_shape, leaf.shape, var, suffix)}]"
+            lines.append(f"const {t} v{k} = {value};")
         names.append(f"v{k}")
     for j, (op, refs, resolved, out_dtype) in enumerate(nodes):
         symbol = f"v{len(leaves) + j}"
@@ -174,20 +204,62 @@ def _body(root_shape, leaves, nodes, var="i"):
 
 
 def elementwise_source(root_shape, leaves, nodes, out_dtype):
+    """One thread per VECTOR consecutive elements in each of
+    ELEMENTS_PER_THREAD groups (a wave's group is 256 consecutive elements).
+    A group whose operands all sit at 4-element alignment reads leaves that
+    equal the root or repeat along leading axes (a bias) and writes the
+    output with one vector access each (16 bytes for 4-byte types); other
+    leaves, the tail and misaligned operands go element by element. Every
+    element computes the same expression as in the element-by-element form,
+    so the bits do not depend on the path."""
     count = prod(root_shape)
-    params, lines, result = _body(root_shape, leaves, nodes)
-    params.append(f"{ctype(out_dtype)}* __restrict__ out")
-    body = "\n      ".join(lines)
-    span = BLOCK * ELEMENTS_PER_THREAD
+    span = BLOCK * ELEMENTS_PER_THREAD * VECTOR
+    small = count + span < 2**32
+    idx, suffix = ("unsigned", "U") if small else ("long long", "LL")
+    t_out = ctype(out_dtype)
+    params, lines, result = _body(root_shape, leaves, nodes, "i", suffix=suffix)
+    params.append(f"{t_out}* __restrict__ out")
+    scalar_body = "\n          ".join(lines)
+    rows = [k for k, leaf in enumerate(leaves) if not leaf.scalar and _rows_of_four(root_shape, leaf.shape)]
+    aligned = " && ".join(
+        [f"((unsigned long long)x{k} % {VECTOR * leaves[k].dtype.itemsize}U == 0)" for k in rows]
+        + [f"((unsigned long long)out % {VECTOR * out_dtype.itemsize}U == 0)"]
+    )
+    loads = "\n        ".join(
+        f"{ctype(leaves[k].dtype)} l{k}[{VECTOR}]; pacho_load4(x{k} + "
+        f"({_broadcast_offset(root_shape, leaves[k].shape, 'i0', suffix)}), l{k});"
+        for k in rows
+    )
+    per_element = []
+    for e in range(VECTOR):
+        def leaf_value(k, e=e):
+            if k in rows:
+                return f"l{k}[{e}]"
+            return f"x{k}[{_broadcast_offset(root_shape, leaves[k].shape, f'(i0 + {e}{suffix})', suffix)}]"
+
+        _, element_lines, element_result = _body(root_shape, leaves, nodes, leaf_value=leaf_value, suffix=suffix)
+        per_element.append("{\n          " + "\n          ".join(element_lines) + f"\n          r[{e}] = {element_result};\n        }}")
+    vector_body = "\n        ".join(per_element)
     source = f"""{_PRELUDE}
 extern "C" __global__ __launch_bounds__({BLOCK}) void pacho_elementwise({", ".join(params)}) {{
-  const long long base = (long long)blockIdx.x * {span}LL + threadIdx.x;
+  const bool aligned = {aligned};
 #pragma unroll
   for (int u = 0; u < {ELEMENTS_PER_THREAD}; ++u) {{
-    const long long i = base + (long long)u * {BLOCK}LL;
-    if (i < {count}LL) {{
-      {body}
-      out[i] = {result};
+    const {idx} i0 = (({idx})(blockIdx.x * {ELEMENTS_PER_THREAD}U + u) * {BLOCK}U + threadIdx.x) * {VECTOR}U;
+    if (aligned && i0 + {VECTOR}{suffix} <= {count}{suffix}) {{
+        {loads}
+        {t_out} r[{VECTOR}];
+        {vector_body}
+        pacho_store4(out + i0, r);
+    }} else {{
+#pragma unroll
+      for (int e = 0; e < {VECTOR}; ++e) {{
+        const {idx} i = i0 + e;
+        if (i < {count}{suffix}) {{
+          {scalar_body}
+          out[i] = {result};
+        }}
+      }}
     }}
   }}
 }}
