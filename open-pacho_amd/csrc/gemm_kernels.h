@@ -339,6 +339,10 @@ using Small = Tile<128, 128, 2, 2, 2>;
 // 4-byte LDS-DMA (mode 2 kernels only: 192-row slices are not whole 16-byte
 // DMA chunks per wave).
 using Wide = Tile<256, 192, 2, 4, 1>;
+// 256 x 128, 8 waves of 64 x 64, one workgroup per compute unit: twice the
+// tiles of Big, for products whose Big tiles would fill part of one round
+// while these fill it whole.
+using Half = Tile<256, 128, 4, 2, 1>;
 
 // gfx950 LDS banks, measured with SQ_LDS_BANK_CONFLICT on probe kernels: a
 // ds_read_b128 serves its 64 lanes in four groups of 16 (lane bit 5 and the
@@ -1893,19 +1897,30 @@ void run_f32_config(hp_ctx* ctx, const float* a, const float* b, float* c, int64
   auto run = [&](auto whole, auto cut, bool moved) {
     launch_split<float, BM, BN>(ctx, whole, cut, fix, T, a, b, c, m, n, k, bd, tm, BK, "gemm_f32", moved);
   };
+  // The register-staged loaders (K-strided operands without row DMA, mode 2
+  // operands past the 32-bit DMA offsets) take tiles of THREADS / 2 rows;
+  // other configurations run only where the DMA loaders serve both operands
+  // (callers check the offsets).
+  constexpr bool kStaged = 2 * BM == T && 2 * BN == T;
   if (mode == 0 && rows) {
     run(kernel<CFG, 0, false, TA, TB, kRows>, kernel<CFG, 0, true, TA, TB, kRows>, false);
-  } else if (mode == 0) {
-    run(kernel<CFG, 0, false, TA, TB, false>, kernel<CFG, 0, true, TA, TB, false>, false);
   } else if (mode == 1 && rows) {
     run(kernel<CFG, 1, false, TA, TB, kRows>, kernel<CFG, 1, true, TA, TB, kRows>, true);
-  } else if (mode == 1) {
-    run(kernel<CFG, 1, false, TA, TB, false>, kernel<CFG, 1, true, TA, TB, false>, true);
-  } else if (fits) {
+  } else if (mode == 2 && fits) {
     // 4-byte LDS-DMA of both operands at any alignment, edges loading +0.
     run(kernel<CFG, 2, false, TA, TB, true>, kernel<CFG, 2, true, TA, TB, true>, true);
+  } else if constexpr (kStaged || !kRows) {
+    if (mode == 0) {
+      run(kernel<CFG, 0, false, TA, TB, false>, kernel<CFG, 0, true, TA, TB, false>, false);
+    } else if (mode == 1) {
+      run(kernel<CFG, 1, false, TA, TB, false>, kernel<CFG, 1, true, TA, TB, false>, true);
+    } else if constexpr (kStaged) {
+      run(kernel<CFG, 2, false, TA, TB, false>, kernel<CFG, 2, true, TA, TB, false>, true);
+    } else {
+      hp::fail(HP_E_HIP, "internal: tile configuration without staged loaders");
+    }
   } else {
-    run(kernel<CFG, 2, false, TA, TB, false>, kernel<CFG, 2, true, TA, TB, false>, true);
+    hp::fail(HP_E_HIP, "internal: tile configuration without staged loaders");
   }
 }
 
@@ -2013,6 +2028,25 @@ void run_f32_wide(hp_ctx* ctx, const float* a, const float* b, float* c, int64_t
   hp::check_launch("gemm_f32");
 }
 
+// Half tiles where Big's fill part of one round (all of them cut into
+// stream-K runs and summed by a fixup launch) while Half's fill 7/8 of one
+// round or more, whole, and K holds more than 64 slices. Measured on one
+// MI355X, microseconds Half / before (Big cut by stream-K, or Small):
+//   4096 x 3001 x 2048 367.8 / 381.3, 4097 x 3001 x 2049 385.5 / 406.2,
+//   8192 x 4096 x 1024 477.8 / 493.2, 2048 x 4096 x 4096 477.6 / 491.4,
+//   4096 x 2048 x 1920 244.5 / 261.4, 3840 x 2048 x 2048 250.9 / 257.7;
+// with 64 slices or fewer they are even or behind (2048 x 1024 x 4096
+// 138.0 / 136.0, 4096 x 1024 x 2048 135.3 / 134.0, 4096 x 256 x 2048
+// 41.4 / 41.1).
+inline bool half_tiles(hp_ctx* ctx, int64_t m, int64_t n, int64_t k, int64_t batch) {
+  using f32::Big;
+  using f32::Half;
+  const int64_t cus = ctx->compute_units;
+  const int64_t big = hp::ceil_div(m, Big::BM) * hp::ceil_div(n, Big::BN) * batch;
+  const int64_t half = hp::ceil_div(m, Half::BM) * hp::ceil_div(n, Half::BN) * batch;
+  return big < cus && half <= cus && 8 * half >= 7 * cus && hp::ceil_div(k, f32::BK) > 64;
+}
+
 template <bool TA, bool TB>
 void run_f32_tiles(hp_ctx* ctx, const float* a, const float* b, float* c, int64_t m, int64_t n, int64_t k,
                    const BatchDesc& bd, int64_t batch, int64_t lda, int64_t ldb, int64_t ldc) {
@@ -2021,6 +2055,9 @@ void run_f32_tiles(hp_ctx* ctx, const float* a, const float* b, float* c, int64_
   } else if (wide_tiles(ctx, m, n, batch) &&
              dma_offsets_fit<TA, TB>(k, lda, ldb, f32::Wide::BM, f32::Wide::BN)) {
     run_f32_wide<TA, TB>(ctx, a, b, c, m, n, k, bd, batch, lda, ldb, ldc);
+  } else if (half_tiles(ctx, m, n, k, batch) &&
+             dma_offsets_fit<TA, TB>(k, lda, ldb, f32::Half::BM, f32::Half::BN)) {
+    run_f32_config<f32::Half, TA, TB>(ctx, a, b, c, m, n, k, bd, batch, lda, ldb, ldc);
   } else if (small_tiles(ctx, m, n, k, batch)) {
     run_f32_config<f32::Small, TA, TB>(ctx, a, b, c, m, n, k, bd, batch, lda, ldb, ldc);
   } else {

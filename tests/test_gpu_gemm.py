@@ -452,6 +452,43 @@ def test_wide_tiles_against_float64_and_deterministic(hip, ta, tb, batch, m, n, 
         np.testing.assert_array_equal(got, eager)
 
 
+# ---- 256 x 128 tiles (eight waves of 64 x 64): products whose 256 x 256
+# tiles would fill part of one round (and be cut by stream-K) while these
+# fill it whole, with more than 64 K slices. Modes 0 (whole tiles), 1 (M/N
+# edges: edge tiles moved inside) and 2 (a K edge), every operand layout,
+# and one batched product.
+
+HALF_CASES = [
+    ((), 4096, 2048, 1088),
+    ((), 4000, 1900, 1088),
+    ((), 4096, 2048, 1090),
+    ((2,), 2048, 2048, 1088),
+]
+
+
+@pytest.mark.parametrize(
+    "ta,tb,batch,m,n,k",
+    [(ta, tb) + case for case in HALF_CASES for ta, tb in LAYOUTS if not (case[0] and (ta or tb))],
+)  # transposed operands are 2-D
+def test_half_tiles_against_float64_and_deterministic(hip, ta, tb, batch, m, n, k):
+    rng = np.random.default_rng(5 * m + 3 * n + k + 2 * ta + tb)
+    left = rng.uniform(-1, 1, batch + ((k, m) if ta else (m, k))).astype(np.float32)
+    right = rng.uniform(-1, 1, (n, k) if tb else (k, n)).astype(np.float32)
+    a, b = p.asarray(left, backend=hip), p.asarray(right, backend=hip)
+    product = p.compile(lambda x, y: (x.T if ta else x) @ (y.T if tb else y))
+    got = p.asnumpy(product(a, b))
+    np.testing.assert_array_equal(got, p.asnumpy(product(a, b)))
+    op_a = np.swapaxes(left, -1, -2) if ta else left
+    op_b = right.T if tb else right
+    if ta or tb:  # the materialized transposes give the same bits
+        plain_a = p.asarray(np.ascontiguousarray(op_a), backend=hip)
+        plain = plain_a @ p.asarray(np.ascontiguousarray(op_b), backend=hip)
+        np.testing.assert_array_equal(got, p.asnumpy(plain))
+    want = op_a.astype(np.float64) @ op_b.astype(np.float64)
+    scale = np.abs(op_a).astype(np.float64) @ np.abs(op_b).astype(np.float64)
+    assert np.all(np.abs(got - want) <= 4e-7 * np.sqrt(k) * 4 * scale + 1e-30)
+
+
 # ---- odd K (a K-edge slice): the whole K slices of products at least one
 # tile tall and wide load by 16-byte LDS-DMA from 4-byte aligned addresses,
 # the K-edge slice by 4-byte LDS-DMA that zero-fills past K. 256 x 256 tiles
