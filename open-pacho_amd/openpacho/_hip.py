@@ -10,8 +10,11 @@ Protocol (reference backends.py:82-150 and _cuda.py:129-679): ``name``,
 
 Storage is an _Allocation (device pointer + capacity) from the library's
 stream-ordered pool. All work of a backend runs on its single stream, so an
-allocation may be returned while kernels that read it are still queued;
-there is no host-side retention list. Operations never download or fall back
+allocation may be returned while kernels that read it are still queued.
+Returned blocks of the pool's smallest size class (0-d results, short
+vectors) wait in a short host-side list for the next small request instead
+of crossing into the library twice; pool statistics, releases and close()
+hand that list back first. Operations never download or fall back
 to the CPU: a missing library or device raises BackendUnavailableError and a
 failing call raises.
 """
@@ -31,6 +34,11 @@ from .exceptions import BackendUnavailableError, UnsupportedDtypeError
 
 _MAX_ELEMENTS = 2**31 - 1
 _KERNEL_CACHE = 256
+# Blocks up to the library pool's smallest size class (runtime.hip
+# size_class: every request <= 512 bytes gets a 512-byte block) are
+# interchangeable; at most _SMALL_KEPT of them wait on the host for reuse.
+_SMALL_BLOCK = 512
+_SMALL_KEPT = 64
 _C_SCALARS = {
     np.dtype("bool"): ctypes.c_uint8,
     np.dtype("int32"): ctypes.c_int32,
@@ -87,7 +95,7 @@ class _Allocation:
         try:
             if self.ptr:
                 ptr, self.ptr = self.ptr, 0
-                self.backend._release(ptr)
+                self.backend._release(ptr, self.capacity)
         except Exception:  # noqa: BLE001 - interpreter shutdown only
             pass
 
@@ -148,6 +156,7 @@ class HIPBackend:
         # allocation), dead ones dropped whenever the list doubles.
         self._leases = []
         self._lease_prune_at = 1024
+        self._small = []  # returned blocks of <= _SMALL_BLOCK bytes, still live in the library
         self._kernels = OrderedDict()
         self._ctx = None
         self._closed = False
@@ -167,6 +176,7 @@ class HIPBackend:
         self._pool_limit = self.device_info.memory_bytes // 4  # hp_init's default
         # Bound once: the calls of the shortest operations are their cost.
         self._free = self._lib.hp_free
+        self._dot = self._lib.hp_dot
         self._dot_new = self._lib.hp_dot_new
 
     # ---- plumbing ---------------------------------------------------------------
@@ -192,10 +202,21 @@ class HIPBackend:
             self._leases = [ref for ref in leases if ref() is not None]
             self._lease_prune_at = max(1024, 2 * len(self._leases))
 
-    def _release(self, ptr):
+    def _release(self, ptr, capacity):
         with self._lock:
-            if not self._closed:
+            if self._closed:
+                return
+            if capacity <= _SMALL_BLOCK and len(self._small) < _SMALL_KEPT:
+                self._small.append(ptr)
+            else:
                 self._free(self._ctx, ptr)
+
+    def _return_small(self):
+        """Hand the host-side small blocks back to the library pool (called
+        with the backend lock held)."""
+        small, self._small = self._small, []
+        for ptr in small:
+            lib_.check(self._lib, self._free(self._ctx, ptr), "hp_free")
 
     def _launch(self, source, name, grid, operands, out):
         """Compile (cached) and launch an RTC kernel over operands + out."""
@@ -237,6 +258,8 @@ class HIPBackend:
             raise ValueError("Array exceeds GPU indexing limits")
         capacity = max(1, count * dtype.itemsize)
         with self._active():
+            if capacity <= _SMALL_BLOCK and self._small:
+                return _Allocation(self, self._small.pop(), capacity)
             ptr = ctypes.c_void_p()
             self._call("hp_alloc", capacity, ctypes.byref(ptr))
             return _Allocation(self, ptr.value, capacity)
@@ -274,6 +297,7 @@ class HIPBackend:
 
     def release_cached_memory(self):
         with self._active():
+            self._return_small()
             self._call("hp_release_cached")
 
     @property
@@ -289,12 +313,14 @@ class HIPBackend:
         if value < 0:
             raise ValueError("pool limit must be non-negative")
         with self._active():
+            self._return_small()
             self._call("hp_set_pool_limit", value)
         self._pool_limit = value
 
     def pool_stats(self):
         values = [ctypes.c_int64(0) for _ in range(4)]
         with self._active():
+            self._return_small()
             self._call("hp_pool_stats", *(ctypes.byref(v) for v in values))
         keys = ("cached_bytes", "cached_items", "live_bytes", "live_items")
         return dict(zip(keys, (v.value for v in values)))
@@ -418,13 +444,23 @@ class HIPBackend:
 
     def vector_dot(self, a, b):
         """Storage of the 0-d a . b of two non-empty 1-D float vectors of one
-        dtype and length: the result's allocation and the launch are one
-        library call. A short dot costs its host calls, not its kernel."""
+        dtype and length. The result takes a small block waiting on the host
+        when there is one (one library call: the launch), else the allocation
+        and the launch are one call. A short dot costs its host calls, not its
+        kernel."""
         dtype = a._dtype
-        ptr = ctypes.c_void_p()
         with self._lock:
             if self._closed:
                 raise RuntimeError("hip backend is closed")
+            small = self._small
+            if small:
+                block = small.pop()
+                status = self._dot(self._ctx, lib_.DTYPE_CODES[dtype], a._data.ptr, b._data.ptr, block, a._shape[0])
+                if status:
+                    small.append(block)
+                    lib_.check(self._lib, status, "hp_dot")
+                return _Allocation(self, block, dtype.itemsize)
+            ptr = ctypes.c_void_p()
             status = self._dot_new(self._ctx, lib_.DTYPE_CODES[dtype], a._data.ptr, b._data.ptr, a._shape[0], ptr)
             if status:
                 lib_.check(self._lib, status, "hp_dot_new")
@@ -584,6 +620,7 @@ class HIPBackend:
                 if lease is not None:
                     lease.ptr = 0
             self._leases = []
+            self._small = []  # still live in the library: hp_destroy frees them
             for kernel in self._kernels.values():
                 self._lib.hp_rtc_release(self._ctx, kernel)
             self._kernels.clear()

@@ -240,6 +240,41 @@ def test_pool_recycles_and_release_keeps_live_arrays(hip):
     np.testing.assert_array_equal(p.asnumpy(live), np.arange(16, dtype=np.float32))
 
 
+def test_small_blocks_wait_on_host_and_return_to_the_pool(hip):
+    """Returned blocks of <= 512 bytes (one pool size class) are reused from
+    the host without a library call; at most 64 wait there, the rest go back
+    to the pool, and statistics and releases see the pool after the host list
+    is handed back."""
+    from openpacho import _hip
+
+    gc.collect()
+    hip.synchronize()
+    hip.release_cached_memory()
+    base = hip.pool_stats()
+    arrays = [p.full((7,), float(i), dtype=np.float32, backend=hip) for i in range(_hip._SMALL_KEPT + 8)]
+    addresses = {a._data.ptr for a in arrays}
+    assert len(addresses) == len(arrays)
+    del arrays
+    gc.collect()
+    kept = list(hip._small)
+    assert len(kept) == _hip._SMALL_KEPT and set(kept) <= addresses
+    reused = p.full((), 2.5, dtype=np.float64, backend=hip)  # a 0-d float64 takes a float32 vector's block
+    assert reused._data.ptr == kept[-1]
+    assert float(p.asnumpy(reused)) == 2.5
+    x = p.asarray(np.arange(1, 65, dtype=np.float32), backend=hip)
+    dots = [p.dot(x, x) for _ in range(3)]
+    assert len({d._data.ptr for d in dots}) == 3
+    assert all(float(p.asnumpy(d)) == float(np.dot(np.arange(1, 65.0), np.arange(1, 65.0))) for d in dots)
+    del dots, reused, x
+    gc.collect()
+    stats = hip.pool_stats()
+    assert not hip._small
+    assert stats["live_items"] == base["live_items"]
+    assert stats["cached_items"] == base["cached_items"] + len(addresses)
+    hip.release_cached_memory()
+    assert hip.pool_stats()["cached_items"] == 0
+
+
 def test_inflight_free_is_stream_ordered(hip):
     # Free an input right after launching its consumer; the next allocation of
     # the same size may reuse the block but runs after the consumer.
