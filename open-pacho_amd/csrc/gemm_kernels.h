@@ -76,7 +76,13 @@ struct Split {
   int moved;       // edge tiles were computed at tile_origin() (the fixup stores alike)
 };
 
-constexpr int64_t kGroupM = 8;
+// Tile rows per group. An XCD's 32 compute units run 32 consecutive tiles
+// at a time: a 4 x 8 block of tiles, whose A and B panels per K slice its L2
+// fetches once. For the 2:1 tiles (256 x 128, fp64's 256 x 128) that is 20%
+// fewer bytes than an 8 x 4 block (4097 x 3001 x 2049: 251 -> 201 MB of
+// fetches per product), the same for square tiles, and batches of grids four
+// tiles tall or less are whole groups either way; times unchanged.
+constexpr int64_t kGroupM = 4;
 
 // 16-byte operand loads that need only element alignment (rows of an odd K
 // or a view at any element offset): one global_load_dwordx4 all the same.
