@@ -39,9 +39,12 @@ def test_integer_stream_is_bit_exact(hip, seed, start, count):
 
 
 @pytest.mark.parametrize("dtype", ["float32", "float64"])
-@pytest.mark.parametrize("start", [0, 2**32 - 3, 2**32 - 700, 2**64 - 1029])
-@pytest.mark.parametrize("count", [1, 3, 1029, 4096])
+@pytest.mark.parametrize("start", [0, 2**32 - 3, 2**32 - 700, 2**32 - 2053, 2**64 - 1029])
+@pytest.mark.parametrize("count", [1, 3, 1029, 4096, 2058])
 def test_random_and_uniform_are_bit_exact(hip, dtype, start, count):
+    # Counts below, at and past one workgroup's 2048 samples; start
+    # 2^32 - 2053 with count 2058 puts the 2^32 carry inside the last,
+    # partial workgroup.
     if start + count > 2**64:
         pytest.skip("past the counter space")
     for dist, kwargs in (("random", {}), ("uniform", {"low": -3, "high": 7})):
