@@ -1117,22 +1117,16 @@ __device__ __forceinline__ void wait_vm() {
   __builtin_amdgcn_s_waitcnt((kWaitVmcnt0 & ~0xC00Fu) | (N & 15) | ((N >> 4) << 14));
 }
 
-// NB = 2: two LDS buffers per wave, slice t + 2 goes into slice t's buffer
-// once its fragments are read (two workgroups fit a compute unit). NB = 4:
-// four buffers, slice t + 3 goes into slice t - 1's buffer, which no read
-// can still touch, so no wait precedes it and loads run three slices ahead
-// (for one tile per compute unit, where a wave has no neighbour on its SIMD
-// to cover its waits).
-template <bool TA, bool TB, int KW, int NB>
+// KW waves per 64 x 64 tile take every KW-th K slice. Two LDS buffers per
+// wave: slice t + 2 goes into slice t's buffer once its fragments are read.
+template <bool TA, bool TB, int KW>
 __global__ __launch_bounds__(64 * KW) void kernel(const float* __restrict__ A, const float* __restrict__ B,
                                                   float* __restrict__ C, int64_t M, int64_t N, int64_t K,
                                                   BatchDesc bd, TileMap tmap) {
-  static_assert(NB == 2 || NB == 4, "two or four buffers per wave");
+  static_assert(KW == 4 || KW == 8, "four or eight waves per tile");
   // Buffers of every wave: [KW][A slice, B slice].
   __shared__ __attribute__((aligned(16))) float L0[KW * kSlice];
   __shared__ __attribute__((aligned(16))) float L1[KW * kSlice];
-  __shared__ __attribute__((aligned(16))) float L2[NB == 4 ? KW * kSlice : 4];
-  __shared__ __attribute__((aligned(16))) float L3[NB == 4 ? KW * kSlice : 4];
   using OA = Operand<TA>;   // A is K-strided when transposed
   using OB = Operand<!TB>;  // B is K-strided unless transposed
   const int lane = threadIdx.x & 63;
@@ -1174,56 +1168,6 @@ __global__ __launch_bounds__(64 * KW) void kernel(const float* __restrict__ A, c
     }
   };
 
-  if constexpr (NB == 4) {
-    // Slices 0-2 in flight; slice 0 must land before its fragments are read.
-    float* const b2 = L2 + wave * kSlice;
-    float* const b3 = L3 + wave * kSlice;
-    if (count > 0) issue(0, b0);
-    if (count > 1) issue(1, b1);
-    if (count > 2) {
-      issue(2, b2);
-      wait_vm<16>();
-    } else {
-      wait_vm<0>();
-    }
-    read(b0, a0, b0f);
-    // Slice t: slice t + 3 into the buffer of slice t - 1 (pd), wait until
-    // slice t + 1 has landed (only t + 2 and t + 3 may be in flight), read
-    // its fragments, then the MFMAs of slice t. The buffers rotate.
-    auto slice4 = [&](int64_t t, float* pd, const float* nxt, const hpd::f32x4* fa, const hpd::f32x4* fb,
-                      hpd::f32x4* na, hpd::f32x4* nb) {
-      if (t + 3 < count) {
-        issue(t + 3, pd);
-        wait_vm<16>();
-      } else {
-        wait_vm<0>();
-      }
-      read(nxt, na, nb);
-#pragma unroll
-      for (int i = 0; i < 4; ++i)
-#pragma unroll
-        for (int q = 0; q < 4; ++q)
-#pragma unroll
-          for (int j = 0; j < 4; ++j)
-            acc[i][j] = __builtin_amdgcn_mfma_f32_16x16x4f32(fa[i][q], fb[j][q], acc[i][j], 0, 0, 0);
-    };
-    float *c0 = b0, *c1 = b1, *c2 = b2, *c3 = b3;  // buffers of slices t .. t + 3
-    auto rotate = [&] {
-      float* x = c0;
-      c0 = c1;
-      c1 = c2;
-      c2 = c3;
-      c3 = x;
-    };
-    int64_t t = 0;
-    for (; t + 1 < count; t += 2) {
-      slice4(t, c3, c1, a0, b0f, a1, b1f);
-      rotate();
-      slice4(t + 1, c3, c1, a1, b1f, a0, b0f);
-      rotate();
-    }
-    if (t < count) slice4(t, c3, c1, a0, b0f, a1, b1f);
-  } else {
   if (count > 0) issue(0, b0);
   if (count > 1) issue(1, b1);
   wait_vm<0>();
@@ -1254,7 +1198,6 @@ __global__ __launch_bounds__(64 * KW) void kernel(const float* __restrict__ A, c
     slice(t + 1, b1, b0, a1, b1f, a0, b0f);
   }
   if (t < count) slice(t, b0, b1, a0, b0f, a1, b1f);
-  }
 
   // Sum the KW accumulator tiles in wave order: waves [0, KW/2) stage theirs
   // in L0, the rest in L1 (16 KB each), then every thread adds whole
@@ -1973,9 +1916,11 @@ bool narrow_fits(const float* a, const float* b, const BatchDesc& bd, int64_t m,
 //   1024^3 90 / 67, 1024 x 1024 x 2048 97 / 86, 2048 x 2048 x 512 90 / 82;
 //   1024 x 1024 x 4096 105 / 105, 2048 x 2048 x 1024 101 / 103,
 //   1536^3 78 / 95, 512 x 512 x 8192 27 / 55, 8 x 1024^3 106 / 119.
-// Four waves per tile (two workgroups per compute unit) beat eight (one) on
-// every one of these shapes.
-constexpr int kNarrowWaves = 4;
+// Waves per tile: eight (two per SIMD; their 136 KiB of LDS leave room for
+// one workgroup per compute unit) where there is one tile per compute unit,
+// else four (two workgroups per compute unit). Against four waves, us per
+// product: 1024^3 20.8 -> 20.3 and 1024 x 1024 x 2048 37.3 -> 36.3 with
+// eight; 2048 x 2048 x 512 (four tiles per compute unit) 39.7 against 47.0.
 
 inline bool narrow_tiles(hp_ctx* ctx, int64_t m, int64_t n, int64_t k, int64_t batch) {
   const int64_t cus = ctx->compute_units;
@@ -1991,13 +1936,10 @@ void run_f32_narrow(hp_ctx* ctx, const float* a, const float* b, float* c, int64
                     const BatchDesc& bd, int64_t batch, int64_t lda, int64_t ldb, int64_t ldc) {
   TileMap tm;
   prepare(m, n, batch, narrow::T, narrow::T, tm, lda, ldb, ldc);
-  // One tile per compute unit: four buffers per wave (loads three slices
-  // ahead, one workgroup per compute unit); more tiles: two, so that two
-  // workgroups share a compute unit.
   if (tm.total <= ctx->compute_units)
-    narrow::kernel<TA, TB, kNarrowWaves, 4><<<tm.total, 64 * kNarrowWaves, 0, ctx->stream>>>(a, b, c, m, n, k, bd, tm);
+    narrow::kernel<TA, TB, 8><<<tm.total, 64 * 8, 0, ctx->stream>>>(a, b, c, m, n, k, bd, tm);
   else
-    narrow::kernel<TA, TB, kNarrowWaves, 2><<<tm.total, 64 * kNarrowWaves, 0, ctx->stream>>>(a, b, c, m, n, k, bd, tm);
+    narrow::kernel<TA, TB, 4><<<tm.total, 64 * 4, 0, ctx->stream>>>(a, b, c, m, n, k, bd, tm);
   hp::check_launch("gemm_f32");
 }
 

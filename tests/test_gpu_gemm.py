@@ -370,12 +370,13 @@ def test_padding_preserves_special_values_and_signed_zero(hip):
 # ---- narrow 64 x 64 tiles: short products with M, N multiples of 64 and K
 # of 16 that give one to four such tiles per compute unit (256 to 1024 on
 # MI355X) and at most 2^23 multiply-adds per compute unit. Each tile is one
-# workgroup whose four waves take every fourth K slice and add their tiles
-# in wave order, so a wave may own one slice or none.
+# workgroup whose waves (eight at one tile per compute unit, else four) take
+# every eighth (fourth) K slice and add their tiles in wave order, so a wave
+# may own one slice or none.
 
 NARROW_CASES = [
-    ((), 1024, 1024, 16),  # one slice: three waves own none
-    ((), 1024, 1024, 48),  # three slices: one wave owns none
+    ((), 1024, 1024, 16),  # one slice: seven of eight waves own none
+    ((), 1024, 1024, 48),  # three slices: five waves own none
     ((), 1024, 1024, 1024),
     ((), 2048, 512, 2048),  # long K: 32 slices per wave
     ((), 1024, 2048, 80),  # two tiles per compute unit
