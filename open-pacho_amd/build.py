@@ -70,11 +70,12 @@ def _resources(lines):
     return kernels
 
 
-# Per-unit flags. The fp32 GEMM units keep MFMA accumulators in VGPRs: with
-# one wave per SIMD (the narrow kernel's four-buffer form, LDS-bound to one
-# workgroup per compute unit) the compiler otherwise put them in AGPRs and
-# copied them to VGPRs and back every slice. The other kernels of these units
-# compile to the same code either way.
+# Per-unit flags. The fp32 GEMM units keep MFMA accumulators in VGPRs. The
+# flag came with an earlier one-wave-per-SIMD form of the narrow kernel, where
+# the compiler otherwise put them in AGPRs and copied them to VGPRs and back
+# every slice. Now it changes only register assignment (in the four-wave
+# narrow kernel and the 256 x 256 mode-2 kernel); every kernel of these units
+# has been measured with it.
 UNIT_FLAGS = {f"gemm_f32_{layout}": ["-mllvm", "-amdgpu-mfma-vgpr-form=1"] for layout in ("nn", "nt", "tn", "tt")}
 
 
