@@ -154,3 +154,15 @@ def test_fused_mlp_epilogue_source_compiles_and_keeps_per_node_rounding():
     assert "tanh" in source and "% 1024LL" in source
     status, log = _compiles(source)
     assert status == 0, log
+
+
+def test_host_small_blocks_match_the_pool_smallest_size_class():
+    # The backend hands any waiting small block to any request of at most
+    # _SMALL_BLOCK bytes, which is sound only while every such request gets a
+    # block of the pool's smallest size class (runtime.hip size_class).
+    from openpacho import _hip
+
+    source = (ROOT / "open-pacho_amd" / "csrc" / "runtime.hip").read_text()
+    match = re.search(r"if \(bytes <= (\d+)\) return (\d+);", source)
+    assert match, "size_class's smallest class not found"
+    assert int(match.group(1)) == int(match.group(2)) == _hip._SMALL_BLOCK
